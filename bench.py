@@ -1,0 +1,225 @@
+#!/usr/bin/env python3
+"""Throughput of the fused PLE path on one MI355X.
+
+A step is one forward (bin search + interpolated prefix table + bias) and one
+backward (dx, dW, db) of the fused operators over one batch of the headline
+workload (configs[1]: N=65536, F=128, 48 bins, d=32, fp32), inputs resident in
+HBM before the timed region starts.  Prints ONE JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--config 1] [--mode fwdbwd|fwd]
+                    [--no-cpu-baseline]
+
+Timing follows the reference harness's discipline (warm-up, then timed
+repetitions between device events on the stream the kernels run on).  The
+``roofline`` object prices the dominant kernel's algorithmic bytes per launch
+against MI355X's 8 TB/s HBM peak; ``cpu_baseline`` times the dense upstream
+CPU algorithm (``oracle/dense_torch.py``) on a bounded sample on the host
+cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+REPO = os.path.dirname(os.path.abspath(__file__))
+
+
+def _parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=1)
+    ap.add_argument("--mode", choices=("fwdbwd", "fwd"), default="fwdbwd")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=4096, help="rows of the workload timed on the CPU")
+    return ap.parse_args()
+
+
+def _traffic(kernel: str, workload: str):
+    """HBM bytes per launch measured by rocprofv3 PMC runs, if committed."""
+    path = os.path.join(REPO, "profiles", f"traffic_{kernel}_{workload}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        return json.load(fh).get("bytes_per_launch")
+
+
+def _cpu_baseline(w, n_rows: int):
+    import numpy as np
+    import torch
+
+    from oracle.dense_torch import DensePLE
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    rows = min(n_rows, w.x.shape[0])
+    x = torch.from_numpy(np.ascontiguousarray(w.x[:rows]))
+    g = torch.randn((rows, w.x.shape[1], w.weight.shape[2]), generator=torch.Generator().manual_seed(0))
+    m = DensePLE(w.bins, w.weight, w.bias)
+    for _ in range(2):
+        m.forward_backward(x, g)
+    times = []
+    t_end = time.perf_counter() + 20.0
+    while len(times) < 10 and (time.perf_counter() < t_end or len(times) < 3):
+        t0 = time.perf_counter()
+        m.forward_backward(x, g)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    return {
+        "value": rows / med,
+        "unit": "samples/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{rows} of {w.x.shape[0]} rows of {w.name}, dense upstream algorithm in torch fp32 "
+                  f"(addcmul/clamp/cat/bmm/+bias, autograd fwd+bwd), median of {len(times)}",
+    }
+
+
+def main():
+    args = _parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} (WORLD_SIZE={world}) is not supported: "
+              "this path is a single-device operator and the run uses one GPU", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import piecewiselinearembeddings_optimized_amd  # noqa: F401  (registers the HIP ops)
+    from piecewiselinearembeddings_optimized_amd import workloads
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    dev = torch.device("cuda:0")
+    ops = torch.ops.rtdl_num_embeddings_cuda
+
+    w = workloads.make(args.config)
+    n, f, bmax, d = w.shape
+    quant = torch.bfloat16 if w.quant == "bf16" else torch.float32
+    out_bytes = 2 if w.quant == "bf16" else 4
+    x = torch.from_numpy(w.x).to(dev)
+    e = torch.from_numpy(w.edges).to(dev)
+    iw = torch.from_numpy(w.inv_widths).to(dev)
+    nb = torch.from_numpy(w.n_bins).to(dev)
+    wt = torch.from_numpy(w.weight).to(dev)
+    bt = torch.from_numpy(w.bias).to(dev)
+    g = torch.randn((n, f, d), device=dev, generator=torch.Generator(dev).manual_seed(0)).to(quant)
+
+    def fwd():
+        if quant == torch.float32:
+            return ops.forward_with_bias(x, e, iw, nb, wt, bt, torch.float32)
+        return ops.forward(x, e, iw, nb, wt, quant)
+
+    def bwd(idx):
+        if quant == torch.float32:
+            return ops.backward_with_bias(g, x, e, iw, nb, wt, idx, torch.float32, True, True, True)
+        return ops.backward(g, x, e, iw, nb, wt, idx, True, True)
+
+    # warm-up (also populates the caching allocator)
+    for _ in range(max(args.warmup, 1)):
+        out, idx = fwd()
+        if args.mode == "fwdbwd":
+            bwd(idx)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    # per-pass event timing on the launch stream
+    def time_pass(fn, reps):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in ev:
+            a.record(stream)
+            fn()
+            b.record(stream)
+        torch.cuda.synchronize()
+        ts = sorted(a.elapsed_time(b) for a, b in ev)
+        return sum(ts) / len(ts), ts[len(ts) // 2]
+
+    fwd_avg_ms, fwd_med_ms = time_pass(fwd, args.steps)
+    _, idx = fwd()
+    bwd_avg_ms = bwd_med_ms = 0.0
+    if args.mode == "fwdbwd":
+        bwd_avg_ms, bwd_med_ms = time_pass(lambda: bwd(idx), args.steps)
+
+    # the timed region: K whole steps, synchronised on both sides
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t0.record(stream)
+    for _ in range(args.steps):
+        out, idx = fwd()
+        if args.mode == "fwdbwd":
+            bwd(idx)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    step_ms = t0.elapsed_time(t1) / args.steps
+    value = n / (step_ms * 1e-3)
+
+    fwd_bytes, bwd_bytes = workloads.algorithmic_bytes(n, f, bmax, d, out_bytes=out_bytes)
+    kernels = {
+        "ple_fwd_kernel": {"ms": fwd_avg_ms, "bytes": fwd_bytes},
+    }
+    if args.mode == "fwdbwd":
+        kernels["backward_op"] = {"ms": bwd_avg_ms, "bytes": bwd_bytes}
+    for k, v in kernels.items():
+        v["GB/s"] = v["bytes"] / (v["ms"] * 1e-3) / 1e9
+        v["frac"] = v["GB/s"] / HBM_PEAK_GBS
+    dom_name = max(kernels, key=lambda k: kernels[k]["ms"])
+    dom = kernels[dom_name]
+    total_bytes = fwd_bytes + (bwd_bytes if args.mode == "fwdbwd" else 0)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = _cpu_baseline(w, args.cpu_sample)
+
+    metric = ("fwd+bwd samples/s (B=65536,F=128,48 bins,d=32) + achieved HBM GB/s" if args.config == 1
+              else f"{'fwd+bwd' if args.mode == 'fwdbwd' else 'fwd'} samples/s ({w.name})")
+    line = {
+        "metric": metric if args.mode == "fwdbwd" else metric.replace("fwd+bwd", "fwd"),
+        "value": value,
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if w.quant == "f32" else "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": w.name, "N": n, "F": f, "bins": bmax, "d": d, "mode": args.mode,
+            "path": "torch.ops.rtdl_num_embeddings_cuda.forward_with_bias/backward_with_bias -> C ABI -> HIP",
+        },
+        "achieved_GBps": total_bytes / (step_ms * 1e-3) / 1e9,
+        "hbm_frac": total_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "fwd_ms": fwd_avg_ms,
+        "fwd_median_ms": fwd_med_ms,
+        "bwd_ms": bwd_avg_ms,
+        "bwd_median_ms": bwd_med_ms,
+        "kernels": kernels,
+        "roofline": {
+            "kernel": dom_name,
+            "bound": "hbm",
+            "achieved": dom["GB/s"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": dom["frac"],
+            "traffic": _traffic(dom_name, w.name),
+            "algorithmic_bytes": dom["bytes"],
+        },
+        "cpu_baseline": cpu,
+        "wall_s_timed": wall,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

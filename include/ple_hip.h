@@ -1,0 +1,121 @@
+/*
+ * C ABI of the MI355X (gfx950) piecewise-linear-embedding kernels.
+ *
+ * Plain pointers and sizes only; every device pointer refers to memory on the
+ * device that is current on the calling thread, and every launch is enqueued
+ * on `stream` (a hipStream_t; NULL = the null stream).  No entry point
+ * allocates device memory or synchronises the host: scratch space is passed in
+ * by the caller (see ple_backward_workspace_bytes).
+ *
+ * Return value: PLE_OK (0), a negative PLE_E_* argument error, or a positive
+ * hipError_t from the launch.  ple_error_string() names every code.
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   ple_forward_launch   <- ple_forward_cuda   csrc/forward_cuda.cu:687-860
+ *                           (registered at csrc/ops.cpp:35-44, :62-75)
+ *   ple_backward_launch  <- ple_backward_cuda  csrc/backward_cuda.cu:1528-1725
+ *                           (registered at csrc/ops.cpp:46-58, :62-75)
+ * The reference exposes these only through the torch dispatcher; this ABI is
+ * the layer under this build's own dispatcher registration, and is what a
+ * ctypes / cgo / JNI binding would call.
+ */
+#ifndef PLE_HIP_H_
+#define PLE_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types */
+enum {
+    PLE_DTYPE_F32 = 0,
+    PLE_DTYPE_F16 = 1,
+    PLE_DTYPE_BF16 = 2,
+};
+
+/* error codes (negative: rejected before any launch) */
+enum {
+    PLE_OK = 0,
+    PLE_E_NULL_POINTER = -1,
+    PLE_E_BAD_SHAPE = -2,
+    PLE_E_BAD_DTYPE = -3,
+    PLE_E_BAD_INDEX_WIDTH = -4,
+    PLE_E_TOO_LARGE = -5,
+    PLE_E_WORKSPACE = -6,
+    PLE_E_UNSUPPORTED = -7,
+    PLE_E_MISALIGNED = -8,
+};
+
+/* Bytes of bin index per (sample, feature) for a given max_n_bins:
+ * 1 up to 256 bins, 2 up to 32768, else 4 (reference _meta.py:14-19). */
+int ple_bin_index_bytes(int64_t max_n_bins);
+
+/*
+ * Forward: for every (n, f)
+ *   k      = searchsorted(bin_edges[f, :n_bins[f]+1], x[n, f], right) - 1,
+ *            clamped to [0, n_bins[f]-1]                 -> bin_indices[n, f]
+ *   frac   = (x[n, f] - bin_edges[f, k]) * inv_bin_widths[f, k]
+ *   r      = fma(q(frac), q(weight[f, phys(k), :]), sum_{j<k} q(weight[f, j, :]))
+ *   out    = round_quant(r) (+ bias[f, :])               -> output[n, f, :]
+ * with q / round_quant = round trip through quant_dtype and
+ * phys(k) = (k == n_bins[f]-1) ? max_n_bins-1 : k.
+ *
+ *   x               float32 [N, F]
+ *   bin_edges       float32 [F, B+1]  (+inf padded past n_bins[f])
+ *   inv_bin_widths  float32 [F, B]    (0 padded)
+ *   n_bins          int32   [F]       (1 <= n_bins[f] <= B)
+ *   weight          float32 [F, B, D]
+ *   bias            float32 [F, D] or NULL (added after quantisation)
+ *   output          output_dtype [N, F, D]
+ *   bin_indices     [N, F] of ple_bin_index_bytes(B) bytes each (uint8 /
+ *                   int16 / int32)
+ *   quant_dtype     PLE_DTYPE_* used for q() and round_quant()
+ *   output_dtype    PLE_DTYPE_* of the stored output
+ * N may be 0 (no launch).  F, B, D >= 1.
+ */
+int ple_forward_launch(const float *x, const float *bin_edges, const float *inv_bin_widths,
+                       const int32_t *n_bins, const float *weight, const float *bias,
+                       void *output, void *bin_indices, int64_t N, int64_t F, int64_t B,
+                       int64_t D, int quant_dtype, int output_dtype, void *stream);
+
+/* Scratch bytes ple_backward_launch needs for these sizes (0 is possible). */
+size_t ple_backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D);
+
+/*
+ * Backward of ple_forward_launch.
+ *   grad_x[n, f]  = iw_k * <g, q(W[f, phys(k)])>
+ *                   + [k > 0 and x == e_k] * iw_{k-1} * <g, q(W[f, k-1])>
+ *   grad_weight[f, phys(k)] = sum_{bin=k} q(frac) g + sum_{bin>k} g
+ *                   (slots no bin maps to are written as 0)
+ *   grad_bias[f]  = sum_n grad_output[n, f]
+ * where g = grad_output rounded through quant_dtype (identity for F32).
+ * Each of grad_x / grad_weight / grad_bias may be NULL (not computed).
+ * Reductions are deterministic: a fixed summation order, no atomics on
+ * floating-point data.
+ *
+ *   grad_output     grad_dtype [N, F, D]
+ *   bin_indices     as produced by ple_forward_launch
+ *   workspace       >= ple_backward_workspace_bytes(N, F, B, D) bytes,
+ *                   256-byte aligned, contents need not be initialised
+ */
+int ple_backward_launch(const void *grad_output, const float *x, const float *bin_edges,
+                        const float *inv_bin_widths, const int32_t *n_bins,
+                        const float *weight, const void *bin_indices, float *grad_x,
+                        float *grad_weight, float *grad_bias, int64_t N, int64_t F,
+                        int64_t B, int64_t D, int grad_dtype, int quant_dtype,
+                        void *workspace, size_t workspace_bytes, void *stream);
+
+/* Human-readable name of a return code (static storage). */
+const char *ple_error_string(int code);
+
+/* ABI version of this header: (major << 16) | minor. */
+int ple_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PLE_HIP_H_ */

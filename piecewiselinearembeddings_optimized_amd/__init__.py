@@ -1,0 +1,24 @@
+"""MI355X-native fused piecewise-linear embeddings (PLE).
+
+Drop-in for the reference package ``rtdl_num_embeddings_cuda`` (also
+importable under that name): the same ``torch.ops.rtdl_num_embeddings_cuda``
+operators, FakeTensor and autograd registrations, and the
+``CudaPiecewiseLinearEmbeddings`` module, running hand-written HIP kernels for
+gfx950 (``csrc/ple_kernels.hip``) behind the C ABI of ``include/ple_hip.h``.
+
+Import order follows the reference (``__init__.py:3-7`` there): the native
+registrations first, then the fake kernels, then autograd, then the module.
+"""
+
+import torch  # noqa: F401  (loads the HIP runtime the extension links against)
+
+from . import _C as _C  # noqa: F401
+from . import _meta as _meta  # noqa: F401
+from . import _autograd as _autograd  # noqa: F401
+from .module import CudaPiecewiseLinearEmbeddings
+
+__all__ = [
+    "CudaPiecewiseLinearEmbeddings",
+]
+
+__version__ = "0.2.0.dev0"

@@ -1,0 +1,210 @@
+"""Boundary checks that need no GPU: the C ABI library and its exports, the
+operator schemas, the FakeTensor contract, the module surface and its CPU
+path (the dense upstream formulation) against the oracle."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import warnings
+
+import numpy as np
+import pytest
+import torch
+
+import piecewiselinearembeddings_optimized_amd as pkg
+from oracle import ple_oracle as po
+from tests.ple_cases import (
+    BIN_CASE_NAMES, FORWARD_ATOL, FORWARD_RTOL, GRAD_ATOL, GRAD_RTOL, init_parameters_, make_bins,
+    sample_features,
+)
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "ple_hip.h")
+LIB = os.path.join(REPO, "piecewiselinearembeddings_optimized_amd", "libple_hip.so")
+
+REFERENCE_SCHEMAS = {
+    # reference csrc/ops.cpp:35-58
+    "forward": "rtdl_num_embeddings_cuda::forward(Tensor x, Tensor bin_edges, Tensor inv_bin_widths, "
+               "Tensor n_bins, Tensor weight, ScalarType output_dtype) -> (Tensor output, Tensor bin_indices)",
+    "backward": "rtdl_num_embeddings_cuda::backward(Tensor grad_output, Tensor x, Tensor bin_edges, "
+                "Tensor inv_bin_widths, Tensor n_bins, Tensor weight, Tensor bin_indices, bool compute_grad_x, "
+                "bool compute_grad_weight) -> (Tensor grad_x, Tensor grad_weight)",
+}
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ple_[a-z_0-9]+)\s*\(", text)))
+
+
+def _lib():
+    return ctypes.CDLL(LIB)
+
+
+def test_library_exports_every_declared_symbol():
+    names = _header_functions()
+    assert {"ple_forward_launch", "ple_backward_launch", "ple_backward_workspace_bytes"} <= set(names)
+    lib = _lib()
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_host_only_entry_points():
+    lib = _lib()
+    lib.ple_bin_index_bytes.argtypes = [ctypes.c_int64]
+    assert [lib.ple_bin_index_bytes(b) for b in (1, 256, 257, 32768, 32769)] == [1, 1, 2, 2, 4]
+    lib.ple_error_string.restype = ctypes.c_char_p
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8):
+        assert lib.ple_error_string(code)
+    assert lib.ple_abi_version() >> 16 == 1
+    assert pkg._C.abi_version() == lib.ple_abi_version()
+
+
+def test_c_abi_rejects_bad_arguments_without_launching():
+    lib = _lib()
+    p = ctypes.c_void_p
+    i64 = ctypes.c_int64
+    lib.ple_forward_launch.argtypes = [p, p, p, p, p, p, p, p, i64, i64, i64, i64, ctypes.c_int, ctypes.c_int, p]
+    dummy = p(256)
+    args = [dummy] * 5 + [None, dummy, dummy]
+    assert lib.ple_forward_launch(*args, 4, 0, 3, 2, 0, 0, None) == -2       # F = 0
+    assert lib.ple_forward_launch(*args, 4, 2, 3, 65, 0, 0, None) == -5      # D > 64
+    assert lib.ple_forward_launch(*args, 4, 2, 3, 2, 9, 0, None) == -3       # bad dtype
+    assert lib.ple_forward_launch(*args, 0, 2, 3, 2, 0, 0, None) == 0        # empty batch: no launch
+    nulls = [None] * 8
+    assert lib.ple_forward_launch(*nulls, 4, 2, 3, 2, 0, 0, None) == -1
+    lib.ple_backward_launch.argtypes = [p, p, p, p, p, p, p, p, p, p, i64, i64, i64, i64, ctypes.c_int,
+                                        ctypes.c_int, p, ctypes.c_size_t, p]
+    assert lib.ple_backward_launch(*[None] * 10, 4, 2, 3, 2, 0, 0, None, 0, None) == 0   # nothing requested
+    assert lib.ple_backward_launch(*[None] * 7, dummy, None, None, 4, 2, 3, 2, 0, 0, None, 0, None) == -1
+
+
+def test_operator_schemas_match_reference():
+    ops = torch.ops.rtdl_num_embeddings_cuda
+    for name, schema in REFERENCE_SCHEMAS.items():
+        assert str(getattr(ops, name).default._schema) == schema
+    assert hasattr(ops, "forward_with_bias") and hasattr(ops, "backward_with_bias")
+
+
+@pytest.mark.parametrize("bmax,idx_dtype", [(5, torch.uint8), (256, torch.uint8), (300, torch.int16), (40000, torch.int32)])
+def test_fake_tensor_contract(bmax, idx_dtype):
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    ops = torch.ops.rtdl_num_embeddings_cuda
+    with FakeTensorMode(allow_non_fake_inputs=False):
+        x = torch.empty(7, 3, device="cuda")
+        e = torch.empty(3, bmax + 1, device="cuda")
+        iw = torch.empty(3, bmax, device="cuda")
+        nb = torch.empty(3, dtype=torch.int32, device="cuda")
+        w = torch.empty(3, bmax, 5, device="cuda")
+        b = torch.empty(3, 5, device="cuda")
+        out, idx = ops.forward(x, e, iw, nb, w, torch.bfloat16)
+        assert out.shape == (7, 3, 5) and out.dtype == torch.bfloat16
+        assert idx.shape == (7, 3) and idx.dtype == idx_dtype
+        out2, _ = ops.forward_with_bias(x, e, iw, nb, w, b, torch.bfloat16)
+        assert out2.dtype == torch.float32
+        g = torch.empty(7, 3, 5, device="cuda")
+        gx, gw = ops.backward(g, x, e, iw, nb, w, idx, True, False)
+        assert gx.shape == x.shape and gw.shape == (0,)
+        gx, gw, gb = ops.backward_with_bias(g, x, e, iw, nb, w, idx, torch.float32, False, True, True)
+        assert gx.shape == (0,) and gw.shape == w.shape and gb.shape == (3, 5)
+        with pytest.raises(Exception):
+            ops.forward(x.double(), e, iw, nb, w, torch.float32)
+
+
+def test_package_surface():
+    import rtdl_num_embeddings_cuda as r
+
+    assert r.__all__ == ["CudaPiecewiseLinearEmbeddings"]
+    assert r.__version__ == "0.2.0.dev0"
+    assert r._C is pkg._C
+    import rtdl_num_embeddings_cuda._C  # noqa: F401
+
+
+def _module(case, d, activation, version, seed=0):
+    from rtdl_num_embeddings_cuda import CudaPiecewiseLinearEmbeddings
+
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        m = CudaPiecewiseLinearEmbeddings(make_bins(case), d, activation=activation, version=version)
+    init_parameters_(m, seed=seed)
+    return m
+
+
+def test_module_parameters_and_state_dict():
+    a = _module("ragged", 10, False, "A")
+    b = _module("ragged", 10, True, "B")
+    assert set(dict(a.named_parameters())) == {"linear.weight", "linear.bias"}
+    assert set(dict(b.named_parameters())) == {"linear.weight", "linear0.weight", "linear0.bias"}
+    sd = a.state_dict()
+    assert not any(k.startswith("_cuda") for k in sd)
+    assert set(sd) == {"impl.weight", "impl.bias", "impl.mask", "linear.weight", "linear.bias"}
+    assert a.get_output_shape() == torch.Size((4, 10))
+    assert a.linear.weight.shape == (4, 5, 10)
+    c = _module("single_bin", 4, False, "A")
+    assert "impl.single_bin_mask" in c.state_dict()
+    # strict round trip of the trainable state
+    a2 = _module("ragged", 10, False, "A", seed=3)
+    a2.linear.load_state_dict(a.linear.state_dict(), strict=True)
+    assert torch.equal(a2.linear.weight, a.linear.weight)
+
+
+def test_module_buffers_follow_reference_layout():
+    m = _module("ragged", 6, False, "A")
+    bins = [b.numpy() for b in make_bins("ragged")]
+    edges, iw, nb = po.pad_bins(bins)
+    np.testing.assert_array_equal(m._cuda_bin_edges.numpy(), edges)
+    np.testing.assert_array_equal(m._cuda_inv_bin_widths.numpy(), iw)
+    np.testing.assert_array_equal(m._cuda_n_bins.numpy(), nb)
+    assert m._cuda_n_bins.dtype == torch.int32
+
+
+def test_module_constructor_validation():
+    from rtdl_num_embeddings_cuda import CudaPiecewiseLinearEmbeddings
+
+    with pytest.raises(AssertionError):
+        CudaPiecewiseLinearEmbeddings(make_bins("equal"), 65, activation=False, version="A")
+    with pytest.raises(ValueError):
+        CudaPiecewiseLinearEmbeddings([], 8, activation=False, version="A")
+    with pytest.raises(ValueError):
+        CudaPiecewiseLinearEmbeddings([torch.tensor([1.0, 0.0])], 8, activation=False, version="A")
+    with pytest.raises(ValueError):
+        CudaPiecewiseLinearEmbeddings([torch.tensor([0.0, float("nan")])], 8, activation=False, version="A")
+    with pytest.warns(UserWarning):
+        CudaPiecewiseLinearEmbeddings(make_bins("equal"), 8, activation=False)
+
+
+@pytest.mark.parametrize("case", BIN_CASE_NAMES)
+@pytest.mark.parametrize("version", ("A", "B"))
+@pytest.mark.parametrize("activation", (False, True))
+def test_module_cpu_path_matches_oracle(case, version, activation):
+    m = _module(case, 10, activation, version, seed=5)
+    bins = make_bins(case)
+    x = sample_features(bins, batch_size=128, seed=7).requires_grad_(True)
+    out = m(x)
+    tables = po.pad_bins([b.numpy() for b in bins])
+    lin0 = None if m.linear0 is None else (m.linear0.weight.detach().numpy(), m.linear0.bias.detach().numpy())
+    bias = None if m.linear.bias is None else m.linear.bias.detach().numpy()
+    ref, _, _ = po.module_forward(x.detach().numpy(), tables, m.linear.weight.detach().numpy(), bias=bias,
+                                  linear0=lin0, activation=activation)
+    torch.testing.assert_close(out.detach().double(), torch.from_numpy(ref), rtol=FORWARD_RTOL, atol=FORWARD_ATOL)
+    if not activation:
+        g = torch.randn_like(out)
+        out.backward(g)
+        edges, iw, nb = tables
+        idx = po.bin_indices(x.detach().numpy(), edges, nb)
+        r = po.backward(g.numpy(), x.detach().numpy(), edges, iw, nb, m.linear.weight.detach().numpy(), idx)
+        dx = r["dx"] + (0.0 if m.linear0 is None else (g.numpy() * m.linear0.weight.detach().numpy()[None]).sum(-1))
+        torch.testing.assert_close(x.grad.double(), torch.from_numpy(dx), rtol=GRAD_RTOL, atol=GRAD_ATOL)
+        torch.testing.assert_close(m.linear.weight.grad.double(), torch.from_numpy(r["dw"]), rtol=GRAD_RTOL, atol=GRAD_ATOL)
+
+
+def test_module_rejects_bad_shapes_on_cpu():
+    m = _module("equal", 4, False, "A")
+    with pytest.raises(ValueError):
+        m(torch.zeros(4, 3, 1))
+    with pytest.raises(ValueError):
+        m(torch.zeros(4, 2))

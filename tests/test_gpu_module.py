@@ -1,0 +1,147 @@
+"""Module-level parity on the GPU, mirroring the reference's
+``tests/test_correctness.py``: the same bin sets, input sampler, parameter
+initialisation, grid (version x activation x seed x d) and tolerances.
+
+The expected values come from the same module evaluated on the CPU, whose
+path is the dense upstream formulation (addcmul -> clamps -> per-feature
+matmul -> bias), i.e. what the reference compares against.
+"""
+
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+from tests.ple_cases import (
+    AMP_FORWARD_ATOL, AMP_FORWARD_RTOL, AMP_GRAD_ATOL, AMP_GRAD_RTOL, BIN_CASE_NAMES,
+    D_EMBEDDING_VALUES, FORWARD_ATOL, FORWARD_RTOL, GRAD_ATOL, GRAD_RTOL, SEED_VALUES,
+    init_parameters_, make_bins, sample_features,
+)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert torch.cuda.is_available(), "HIP device required"
+    yield
+
+
+def _modules(case_name, d, activation, version, seed):
+    from rtdl_num_embeddings_cuda import CudaPiecewiseLinearEmbeddings
+
+    bins = make_bins(case_name)
+    cpu = CudaPiecewiseLinearEmbeddings(bins, d, activation=activation, version=version)
+    init_parameters_(cpu, seed=seed)
+    gpu = copy.deepcopy(cpu).to("cuda")
+    assert set(dict(gpu.named_parameters())) == set(dict(cpu.named_parameters()))
+    return bins, cpu, gpu
+
+
+GRID = pytest.mark.parametrize(
+    "case_name,version,activation,seed,d",
+    [
+        (c, v, a, s, d)
+        for c in BIN_CASE_NAMES for v in ("A", "B") for a in (False, True)
+        for s in SEED_VALUES for d in D_EMBEDDING_VALUES
+    ],
+)
+
+
+@GRID
+def test_forward_matches_cpu_module(case_name, version, activation, seed, d):
+    bins, cpu, gpu = _modules(case_name, d, activation, version, seed)
+    x = sample_features(bins, batch_size=128, seed=seed + 1000)
+    with torch.no_grad():
+        expected = cpu(x)
+        actual = gpu(x.cuda())
+    assert actual.shape == (128, len(bins), d)
+    assert actual.dtype == expected.dtype
+    assert gpu.get_output_shape() == cpu.get_output_shape()
+    torch.testing.assert_close(actual.cpu(), expected, rtol=FORWARD_RTOL, atol=FORWARD_ATOL)
+
+
+@GRID
+def test_backward_matches_cpu_module(case_name, version, activation, seed, d):
+    bins, cpu, gpu = _modules(case_name, d, activation, version, seed)
+    xb = sample_features(bins, batch_size=128, seed=seed + 2000)
+    xc = xb.clone().requires_grad_(True)
+    xg = xb.cuda().requires_grad_(True)
+    oc, og = cpu(xc), gpu(xg)
+    torch.manual_seed(seed + 3000)
+    g = torch.randn_like(oc)
+    oc.backward(g)
+    og.backward(g.cuda())
+    torch.testing.assert_close(xg.grad.cpu(), xc.grad, rtol=GRAD_RTOL, atol=GRAD_ATOL)
+    torch.testing.assert_close(gpu.linear.weight.grad.cpu(), cpu.linear.weight.grad, rtol=GRAD_RTOL, atol=GRAD_ATOL)
+    if version == "A":
+        torch.testing.assert_close(gpu.linear.bias.grad.cpu(), cpu.linear.bias.grad, rtol=GRAD_RTOL, atol=GRAD_ATOL)
+    else:
+        assert gpu.linear.bias is None
+        torch.testing.assert_close(gpu.linear0.weight.grad.cpu(), cpu.linear0.weight.grad, rtol=GRAD_RTOL, atol=GRAD_ATOL)
+        torch.testing.assert_close(gpu.linear0.bias.grad.cpu(), cpu.linear0.bias.grad, rtol=GRAD_RTOL, atol=GRAD_ATOL)
+
+
+def _amp_reference(cpu, x):
+    """The reference module under bf16 autocast, evaluated on the CPU: PLE
+    branch rounded through bf16 (encoding and weights), fp32 accumulation,
+    bf16 result, then the fp32 bias / residual."""
+    enc = cpu.impl(x)
+    x_ple = (enc.to(torch.bfloat16).float().transpose(0, 1) @ cpu.linear.weight.to(torch.bfloat16).float())
+    x_ple = x_ple.transpose(0, 1).to(torch.bfloat16)
+    out = x_ple.float() + cpu.linear.bias if cpu.linear.bias is not None else x_ple
+    if cpu.activation is not None:
+        out = cpu.activation(out)
+    if cpu.linear0 is not None:
+        out = cpu.linear0(x) + out
+    return out
+
+
+@GRID
+def test_forward_amp_bfloat16_matches(case_name, version, activation, seed, d):
+    bins, cpu, gpu = _modules(case_name, d, activation, version, seed)
+    x = sample_features(bins, batch_size=128, seed=seed + 4000)
+    with torch.no_grad():
+        expected = _amp_reference(cpu, x)
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            actual = gpu(x.cuda())
+    torch.testing.assert_close(actual.float().cpu(), expected.float(), rtol=AMP_FORWARD_RTOL, atol=AMP_FORWARD_ATOL)
+
+
+@GRID
+def test_backward_amp_bfloat16_matches(case_name, version, activation, seed, d):
+    bins, cpu, gpu = _modules(case_name, d, activation, version, seed)
+    xb = sample_features(bins, batch_size=128, seed=seed + 5000)
+    xc = xb.clone().requires_grad_(True)
+    xg = xb.cuda().requires_grad_(True)
+    oc = _amp_reference(cpu, xc)
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        og = gpu(xg)
+    torch.manual_seed(seed + 6000)
+    g = torch.randn(oc.shape, dtype=torch.float32).to(oc.dtype)
+    oc.backward(g)
+    og.backward(g.to(og.dtype).cuda())
+    assert xg.grad.dtype == torch.float32
+    torch.testing.assert_close(xg.grad.cpu(), xc.grad, rtol=AMP_GRAD_RTOL, atol=AMP_GRAD_ATOL)
+    torch.testing.assert_close(gpu.linear.weight.grad.cpu(), cpu.linear.weight.grad, rtol=AMP_GRAD_RTOL, atol=AMP_GRAD_ATOL)
+    if version == "A":
+        torch.testing.assert_close(gpu.linear.bias.grad.cpu(), cpu.linear.bias.grad, rtol=AMP_GRAD_RTOL, atol=AMP_GRAD_ATOL)
+    else:
+        torch.testing.assert_close(gpu.linear0.weight.grad.cpu(), cpu.linear0.weight.grad, rtol=AMP_GRAD_RTOL, atol=AMP_GRAD_ATOL)
+        torch.testing.assert_close(gpu.linear0.bias.grad.cpu(), cpu.linear0.bias.grad, rtol=AMP_GRAD_RTOL, atol=AMP_GRAD_ATOL)
+
+
+def test_module_errors_on_gpu():
+    from rtdl_num_embeddings_cuda import CudaPiecewiseLinearEmbeddings
+
+    m = CudaPiecewiseLinearEmbeddings(make_bins("equal"), 8, activation=False, version="A").cuda()
+    with pytest.raises(TypeError):
+        m(torch.zeros(4, 3, device="cuda", dtype=torch.float64))
+    with pytest.raises(ValueError):
+        m(torch.zeros(3, 4, device="cuda").t())
+    with pytest.raises(ValueError):
+        m(torch.zeros(4, 2, device="cuda"))
+    with pytest.raises(ValueError):
+        m(torch.zeros(4, 3, 1, device="cuda"))
