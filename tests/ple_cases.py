@@ -83,6 +83,15 @@ def with_edge_hits(x: torch.Tensor, bins, every: int = 7) -> torch.Tensor:
     return x
 
 
+def normwise_rel(actual, expected) -> float:
+    """max |a - e| / max |e| over finite entries (relative error of the tensor)."""
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    fin = np.isfinite(e)
+    den = float(np.abs(e[fin]).max()) if fin.any() else 1.0
+    return float(np.abs(a[fin] - e[fin]).max()) / (den if den > 0 else 1.0)
+
+
 def close_scaled(actual, expected, abs_sum, rtol, atol) -> tuple[bool, float]:
     """``|a - e| <= atol + rtol * abs_sum`` elementwise (NaN == NaN, equal infs).
 

@@ -80,8 +80,21 @@ def test_backward_matches_cpu_module(case_name, version, activation, seed, d):
         torch.testing.assert_close(gpu.linear.bias.grad.cpu(), cpu.linear.bias.grad, rtol=GRAD_RTOL, atol=GRAD_ATOL)
     else:
         assert gpu.linear.bias is None
-        torch.testing.assert_close(gpu.linear0.weight.grad.cpu(), cpu.linear0.weight.grad, rtol=GRAD_RTOL, atol=GRAD_ATOL)
-        torch.testing.assert_close(gpu.linear0.bias.grad.cpu(), cpu.linear0.bias.grad, rtol=GRAD_RTOL, atol=GRAD_ATOL)
+        _check_linear0_grads(gpu, xb, g, GRAD_RTOL, GRAD_ATOL)
+
+
+def _check_linear0_grads(gpu, x, g, rtol, atol):
+    """linear0 (x_linear = b0 + w0 * x) is plain PyTorch on both sides; its
+    gradients are sums over the batch, so they are checked against float64
+    with the tolerance scaled by the sum of |terms| (a CPU and a GPU fp32 sum
+    of 128 terms may differ by more than rtol * |sum| under cancellation)."""
+    gd, xd = g.double(), x.double()
+    terms_w = gd * xd[..., None]
+    dw0, dw0_abs = terms_w.sum(0), terms_w.abs().sum(0)
+    db0, db0_abs = gd.sum(0), gd.abs().sum(0)
+    for got, exp, s in ((gpu.linear0.weight.grad, dw0, dw0_abs), (gpu.linear0.bias.grad, db0, db0_abs)):
+        err = (got.cpu().double() - exp).abs()
+        assert bool((err <= atol + rtol * s).all()), float((err / (atol + rtol * s)).max())
 
 
 def _amp_reference(cpu, x):
@@ -129,8 +142,7 @@ def test_backward_amp_bfloat16_matches(case_name, version, activation, seed, d):
     if version == "A":
         torch.testing.assert_close(gpu.linear.bias.grad.cpu(), cpu.linear.bias.grad, rtol=AMP_GRAD_RTOL, atol=AMP_GRAD_ATOL)
     else:
-        torch.testing.assert_close(gpu.linear0.weight.grad.cpu(), cpu.linear0.weight.grad, rtol=AMP_GRAD_RTOL, atol=AMP_GRAD_ATOL)
-        torch.testing.assert_close(gpu.linear0.bias.grad.cpu(), cpu.linear0.bias.grad, rtol=AMP_GRAD_RTOL, atol=AMP_GRAD_ATOL)
+        _check_linear0_grads(gpu, xb, g.float(), AMP_GRAD_RTOL, AMP_GRAD_ATOL)
 
 
 def test_module_errors_on_gpu():
