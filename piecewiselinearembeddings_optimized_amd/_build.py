@@ -36,12 +36,10 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-Wall",
     # Packed fp32 VALU ops stay off (the compiler would otherwise form them
     # from ordinary float code).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-Wl,-soname,libple_hip.so",
 ]
 
 
@@ -67,10 +65,25 @@ def _hipcc() -> str:
     return p
 
 
+KERNEL_SOURCES = ("ple_capi.hip", "ple_forward.hip", "ple_backward.hip")
+
+
 def build_kernels(verbose: bool = False) -> str:
-    src = os.path.join(CSRC, "ple_kernels.hip")
-    tmp = KERNEL_LIB + ".tmp"
-    _run([_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-o", tmp, src], verbose)
+    """One hipcc process per translation unit (in parallel), then the link."""
+    import concurrent.futures as cf
+    import tempfile
+
+    hipcc = _hipcc()
+    with tempfile.TemporaryDirectory(prefix="ple_build_") as tmpdir:
+        objs = [os.path.join(tmpdir, os.path.splitext(s)[0] + ".o") for s in KERNEL_SOURCES]
+        cmds = [[hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", "-o", o, os.path.join(CSRC, s)]
+                for s, o in zip(KERNEL_SOURCES, objs)]
+        with cf.ThreadPoolExecutor(max_workers=len(cmds)) as ex:
+            for fut in [ex.submit(_run, c, verbose) for c in cmds]:
+                fut.result()
+        tmp = KERNEL_LIB + ".tmp"
+        _run([hipcc, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", "-Wl,-soname,libple_hip.so",
+              "-o", tmp, *objs], verbose)
     os.replace(tmp, KERNEL_LIB)
     return KERNEL_LIB
 

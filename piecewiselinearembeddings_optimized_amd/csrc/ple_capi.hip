@@ -1,0 +1,111 @@
+// The extern "C" entry points of include/ple_hip.h: argument checks that need
+// no device, then the forward / backward launchers.
+
+#include "ple_internal.h"
+
+namespace ple {
+
+int device_cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
+}
+
+namespace {
+
+int check_common(int64_t N, int64_t F, int64_t B, int64_t D) {
+    if (N < 0 || F < 1 || B < 1 || D < 1) return PLE_E_BAD_SHAPE;
+    if (F > INT32_MAX / 2 || B > 32766 || D > 64) return PLE_E_TOO_LARGE;
+    if (F * (B + 1) > INT32_MAX / 2 || F * B * 2 * D > INT32_MAX) return PLE_E_TOO_LARGE;
+    if (N > INT64_MAX / (F * D)) return PLE_E_TOO_LARGE;
+    return PLE_OK;
+}
+
+}  // namespace
+}  // namespace ple
+
+extern "C" {
+
+int ple_abi_version(void) { return (1 << 16) | 0; }
+
+int ple_bin_index_bytes(int64_t max_n_bins) { return ple::idx_bytes_for(max_n_bins); }
+
+const char *ple_error_string(int code) {
+    switch (code) {
+        case PLE_OK: return "success";
+        case PLE_E_NULL_POINTER: return "a required pointer is NULL";
+        case PLE_E_BAD_SHAPE: return "invalid shape (need N >= 0 and F, B, D >= 1)";
+        case PLE_E_BAD_DTYPE: return "invalid dtype code";
+        case PLE_E_BAD_INDEX_WIDTH: return "invalid bin index width";
+        case PLE_E_TOO_LARGE: return "sizes exceed the supported range (D <= 64, max_n_bins <= 32766)";
+        case PLE_E_WORKSPACE: return "workspace is NULL, too small or not 256-byte aligned";
+        case PLE_E_UNSUPPORTED: return "combination not supported (dtype pairing, or per-feature tables exceed LDS)";
+        case PLE_E_MISALIGNED: return "pointer misaligned for its element type";
+        default: break;
+    }
+    if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+    return "unknown error";
+}
+
+int ple_forward_launch(const float *x, const float *bin_edges, const float *inv_bin_widths,
+                       const int32_t *n_bins, const float *weight, const float *bias,
+                       void *output, void *bin_indices, int64_t N, int64_t F, int64_t B,
+                       int64_t D, int quant_dtype, int output_dtype, void *stream) {
+    const int rc = ple::check_common(N, F, B, D);
+    if (rc != PLE_OK) return rc;
+    if (!ple::valid_dtype(quant_dtype) || !ple::valid_dtype(output_dtype)) return PLE_E_BAD_DTYPE;
+    if (N == 0) return PLE_OK;
+    if (!x || !bin_edges || !inv_bin_widths || !n_bins || !weight || !output || !bin_indices)
+        return PLE_E_NULL_POINTER;
+    ple::ForwardRequest r;
+    r.x = x; r.edges = bin_edges; r.iw = inv_bin_widths; r.nbins = n_bins; r.weight = weight;
+    r.bias = bias; r.out = output; r.idx = bin_indices;
+    r.N = N; r.F = F; r.B = B; r.D = D;
+    r.quant = quant_dtype; r.out_dtype = output_dtype;
+    r.stream = static_cast<hipStream_t>(stream);
+    return ple::forward_run(r);
+}
+
+size_t ple_backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D) {
+    if (ple::check_common(N, F, B, D) != PLE_OK || N == 0) return 0;
+    return ple::backward_workspace_bytes(N, F, B, D);
+}
+
+int ple_backward_launch(const void *grad_output, const float *x, const float *bin_edges,
+                        const float *inv_bin_widths, const int32_t *n_bins,
+                        const float *weight, const void *bin_indices, float *grad_x,
+                        float *grad_weight, float *grad_bias, int64_t N, int64_t F,
+                        int64_t B, int64_t D, int grad_dtype, int quant_dtype,
+                        void *workspace, size_t workspace_bytes, void *stream) {
+    const int rc = ple::check_common(N, F, B, D);
+    if (rc != PLE_OK) return rc;
+    if (!ple::valid_dtype(grad_dtype) || !ple::valid_dtype(quant_dtype)) return PLE_E_BAD_DTYPE;
+    if (!grad_x && !grad_weight && !grad_bias) return PLE_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (N == 0) {
+        // empty batch: the parameter gradients are zero
+        hipError_t e = hipSuccess;
+        if (grad_weight) e = hipMemsetAsync(grad_weight, 0, sizeof(float) * F * B * D, s);
+        if (e == hipSuccess && grad_bias) e = hipMemsetAsync(grad_bias, 0, sizeof(float) * F * D, s);
+        return e == hipSuccess ? PLE_OK : static_cast<int>(e);
+    }
+    if (!grad_output || !x || !bin_edges || !inv_bin_widths || !n_bins || !weight || !bin_indices)
+        return PLE_E_NULL_POINTER;
+    ple::BackwardRequest r;
+    r.g = grad_output; r.x = x; r.edges = bin_edges; r.iw = inv_bin_widths; r.nbins = n_bins;
+    r.weight = weight; r.idx = bin_indices; r.dx = grad_x; r.dw = grad_weight; r.db = grad_bias;
+    r.N = N; r.F = F; r.B = B; r.D = D;
+    r.grad_dtype = grad_dtype; r.quant = quant_dtype;
+    r.workspace = workspace; r.workspace_bytes = workspace_bytes;
+    r.stream = s;
+    return ple::backward_run(r);
+}
+
+}  // extern "C"

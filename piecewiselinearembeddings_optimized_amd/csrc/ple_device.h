@@ -1,0 +1,174 @@
+// Device-side helpers shared by the PLE kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/ple_hip.h"
+
+namespace ple {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;
+constexpr int kWavesPerBlock = kBlock / kWave;
+constexpr int kNumXcd = 8;
+
+// ---------------------------------------------------------------------------
+// element conversions
+// ---------------------------------------------------------------------------
+
+// float -> bfloat16 -> float, nearest-even; NaN -> quiet NaN.
+__device__ __forceinline__ float bf16_round(float v) {
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return __uint_as_float(0x7fc00000u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return __uint_as_float(u & 0xffff0000u);
+}
+
+__device__ __forceinline__ uint16_t bf16_bits(float v) {
+    return static_cast<uint16_t>(__float_as_uint(bf16_round(v)) >> 16);
+}
+
+__device__ __forceinline__ float f16_round(float v) {
+    return static_cast<float>(static_cast<_Float16>(v));
+}
+
+__device__ __forceinline__ uint16_t f16_bits(float v) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+// Round trip through the quantisation dtype (identity for fp32).
+template <int Q>
+__device__ __forceinline__ float quant(float v) {
+    if constexpr (Q == PLE_DTYPE_BF16) return bf16_round(v);
+    else if constexpr (Q == PLE_DTYPE_F16) return f16_round(v);
+    else return v;
+}
+
+__device__ __forceinline__ float bf16_to_float(uint16_t b) {
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+__device__ __forceinline__ float f16_to_float(uint16_t b) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+
+template <int G>
+__device__ __forceinline__ float load_grad(const void *p, int64_t i) {
+    if constexpr (G == PLE_DTYPE_F32) return static_cast<const float *>(p)[i];
+    else if constexpr (G == PLE_DTYPE_BF16) return bf16_to_float(static_cast<const uint16_t *>(p)[i]);
+    else return f16_to_float(static_cast<const uint16_t *>(p)[i]);
+}
+
+// Loads VEC consecutive gradient elements starting at element i (i is a
+// multiple of VEC; the base is aligned for the vector width).
+template <int G, int VEC>
+__device__ __forceinline__ void load_grad_vec(const void *p, int64_t i, float *out) {
+    if constexpr (G == PLE_DTYPE_F32) {
+        const float *q = static_cast<const float *>(p) + i;
+        if constexpr (VEC == 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(q);
+            out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+        } else if constexpr (VEC == 2) {
+            const float2 v = *reinterpret_cast<const float2 *>(q);
+            out[0] = v.x; out[1] = v.y;
+        } else {
+            out[0] = q[0];
+        }
+    } else {
+        const uint16_t *q = static_cast<const uint16_t *>(p) + i;
+        uint16_t h[VEC];
+        if constexpr (VEC == 4) {
+            const uint2 v = *reinterpret_cast<const uint2 *>(q);
+            h[0] = v.x & 0xffffu; h[1] = v.x >> 16; h[2] = v.y & 0xffffu; h[3] = v.y >> 16;
+        } else if constexpr (VEC == 2) {
+            const uint32_t v = *reinterpret_cast<const uint32_t *>(q);
+            h[0] = v & 0xffffu; h[1] = v >> 16;
+        } else {
+            h[0] = q[0];
+        }
+#pragma unroll
+        for (int t = 0; t < VEC; ++t)
+            out[t] = (G == PLE_DTYPE_BF16) ? bf16_to_float(h[t]) : f16_to_float(h[t]);
+    }
+}
+
+// Stores VEC consecutive outputs as OUT (VEC in {1, 4}).
+template <int OUT, int VEC>
+__device__ __forceinline__ void store_out(void *base, int64_t i, const float *v) {
+    if constexpr (OUT == PLE_DTYPE_F32) {
+        float *p = static_cast<float *>(base) + i;
+        if constexpr (VEC == 4) *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+        else p[0] = v[0];
+    } else {
+        uint16_t h[VEC];
+#pragma unroll
+        for (int t = 0; t < VEC; ++t) h[t] = (OUT == PLE_DTYPE_BF16) ? bf16_bits(v[t]) : f16_bits(v[t]);
+        uint16_t *p = static_cast<uint16_t *>(base) + i;
+        if constexpr (VEC == 4) {
+            uint2 w;
+            w.x = static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16);
+            w.y = static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16);
+            *reinterpret_cast<uint2 *>(p) = w;
+        } else {
+            p[0] = h[0];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bins
+// ---------------------------------------------------------------------------
+
+// searchsorted(edges[0..n], v, side=right) - 1, clamped to [0, n-1].  Every
+// comparison with NaN is false, so NaN walks to the top and lands in bin n-1.
+__device__ __forceinline__ int find_bin(float v, const float *e, int n) {
+    int lo = 0;
+    int hi = n + 1;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (v < e[mid]) hi = mid;
+        else lo = mid + 1;
+    }
+    int k = lo - 1;
+    k = k < 0 ? 0 : k;
+    k = k > n - 1 ? n - 1 : k;
+    return k;
+}
+
+// n_bins and bin indices come from the caller; clamping them keeps every
+// table access inside its row even for inconsistent inputs (valid inputs are
+// unchanged).
+__device__ __forceinline__ int clamp_nbins(int n, int bmax) {
+    return n < 1 ? 1 : (n > bmax ? bmax : n);
+}
+
+__device__ __forceinline__ int clamp_bin(int k, int n) {
+    return k < 0 ? 0 : (k > n - 1 ? n - 1 : k);
+}
+
+// The last real bin's parameters live in slot bmax-1.
+__host__ __device__ __forceinline__ int phys_bin(int k, int n, int bmax) {
+    return k == n - 1 ? bmax - 1 : k;
+}
+
+template <typename IdxT>
+__device__ __forceinline__ int load_idx(const void *p, int64_t i) {
+    return static_cast<int>(static_cast<const IdxT *>(p)[i]);
+}
+
+// Workgroup -> (feature group, sample chunk), XCD aware: workgroup ids are
+// dealt to the XCDs round-robin, so chunks are dealt the same way and all
+// feature groups of one chunk run back to back on one XCD, where they share
+// that XCD's L2 lines of x, of the bin indices and of dx.
+__device__ __forceinline__ bool decode_tile(int bid, int G, int C, int &g, int &c) {
+    const int x8 = bid % kNumXcd;
+    const int L = bid / kNumXcd;
+    g = L % G;
+    c = (L / G) * kNumXcd + x8;
+    return c < C;
+}
+
+}  // namespace ple

@@ -1,0 +1,307 @@
+// Forward kernel of the fused PLE path (gfx950).
+//
+// One workgroup owns a group of FS features and a chunk of samples.  It
+// stages, per feature, the bin edges, the inverse widths and a [bins x 2D]
+// table {prefix of quantised weights | quantised weight row} in LDS, then its
+// four waves stream wave tiles of 64 (sample, feature) pairs: each lane
+// bin-searches one pair in LDS, the pair's (bin, fraction) reaches the lanes
+// that store that pair's D outputs through ds_bpermute, and the outputs leave
+// as 16-byte stores covering whole sample rows of the group.
+//
+// Arithmetic per output element is the reference's (forward_cuda.cu:135-178,
+// 208-283): prefix accumulated in fp32 in bin order, then
+// fma(q(frac), q(W[phys(k)]), prefix[k]), rounded to the output dtype; the
+// optional bias is added in fp32 after that rounding.
+
+#include <stdlib.h>
+
+#include "ple_device.h"
+#include "ple_internal.h"
+
+namespace ple {
+namespace {
+
+struct FwdArgs {
+    const float *x;
+    const float *edges;
+    const float *iw;
+    const int32_t *nbins;
+    const float *weight;
+    const float *bias;
+    void *out;
+    void *idx;
+    int64_t N;
+    int F, B, D;
+    int FS;       // features per workgroup (power of two, FS * D/VEC <= 64)
+    int G;        // feature groups = ceil(F / FS)
+    int C;        // sample chunks (multiple of kNumXcd)
+    int64_t NC;   // samples per chunk
+};
+
+size_t fwd_lds_bytes(int FS, int B, int D) {
+    return 4 * (static_cast<size_t>(FS) * B * 2 * D   // table {prefix | weight}
+                + static_cast<size_t>(FS) * (B + 1)   // edges
+                + static_cast<size_t>(FS) * B         // inverse widths
+                + static_cast<size_t>(FS));           // n_bins
+}
+
+template <int Q, int OUT, bool HAS_BIAS, int VEC, typename IdxT>
+__global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
+    extern __shared__ float smem[];
+    const int FS = a.FS, B = a.B, D = a.D, F = a.F;
+    const int rs = 2 * D;                                   // table row stride
+    float *tbl = smem;
+    float *sedge = tbl + static_cast<size_t>(FS) * B * rs;
+    float *siw = sedge + FS * (B + 1);
+    int *snb = reinterpret_cast<int *>(siw + FS * B);
+
+    int g, c;
+    if (!decode_tile(blockIdx.x, a.G, a.C, g, c)) return;
+    const int f0 = g * FS;
+    const int nfh = min(FS, F - f0);
+    const int64_t n_begin = static_cast<int64_t>(c) * a.NC;
+    const int64_t n_end = min(a.N, n_begin + a.NC);
+    if (n_begin >= n_end) return;
+    const int tid = threadIdx.x;
+
+    // ---- stage the per-feature tables ------------------------------------
+    for (int i = tid; i < FS; i += kBlock) snb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
+    for (int i = tid; i < FS * (B + 1); i += kBlock) {
+        const int fl = i / (B + 1);
+        sedge[i] = fl < nfh ? a.edges[static_cast<int64_t>(f0) * (B + 1) + i] : 0.0f;
+    }
+    for (int i = tid; i < FS * B; i += kBlock) {
+        const int fl = i / B;
+        siw[i] = fl < nfh ? a.iw[static_cast<int64_t>(f0) * B + i] : 0.0f;
+    }
+    __syncthreads();
+
+    const int U = D / VEC;
+    for (int i = tid; i < FS * B * U; i += kBlock) {
+        const int fl = i / (B * U);
+        const int r = i - fl * (B * U);
+        const int k = r / U;
+        const int u = r - k * U;
+        if (fl < nfh) {
+            const int n = snb[fl];
+            if (k < n) {
+                const int p = phys_bin(k, n, B);
+                const float *src = a.weight + ((static_cast<int64_t>(f0 + fl) * B + p) * D + u * VEC);
+                float *dst = tbl + (static_cast<size_t>(fl) * B + k) * rs + D + u * VEC;
+                if constexpr (VEC == 4) {
+                    const float4 w = *reinterpret_cast<const float4 *>(src);
+                    dst[0] = quant<Q>(w.x);
+                    dst[1] = quant<Q>(w.y);
+                    dst[2] = quant<Q>(w.z);
+                    dst[3] = quant<Q>(w.w);
+                } else {
+                    dst[0] = quant<Q>(src[0]);
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // prefix over logical bins, one lane per (feature, column), in bin order
+    for (int col = tid; col < FS * D; col += kBlock) {
+        const int fl = col / D;
+        const int j = col - fl * D;
+        if (fl < nfh) {
+            const int n = snb[fl];
+            float *base = tbl + static_cast<size_t>(fl) * B * rs;
+            float acc = 0.0f;
+            int k = 0;
+            for (; k + 8 <= n; k += 8) {
+                float w[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) w[t] = base[(k + t) * rs + D + j];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    base[(k + t) * rs + j] = acc;
+                    acc += w[t];
+                }
+            }
+            for (; k < n; ++k) {
+                const float w = base[k * rs + D + j];
+                base[k * rs + j] = acc;
+                acc += w;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- stream wave tiles -------------------------------------------------
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    const int SW = kWave / FS;      // samples per wave tile
+    const int Lv = FS * U;          // vector slots per sample row of the group
+    const int R = kWave / Lv;       // sample rows per store instruction
+
+    // pair phase: lane -> (sample p_s, feature p_fl)
+    const int p_s = lane / FS;
+    const int p_fl = lane - p_s * FS;
+    const float *e_row = sedge + p_fl * (B + 1);
+    const float *iw_row = siw + p_fl * B;
+    const int p_n = snb[p_fl];
+    const bool p_fok = p_fl < nfh;
+
+    // store phase: lane -> (row o_s, feature o_fl, vector o_u), fixed per lane
+    const int o_s = lane / Lv;
+    const int o_v = lane - o_s * Lv;
+    const int o_fl = o_v / U;
+    const int o_u = o_v - o_fl * U;
+    const bool o_ok = (o_s < R) && (o_fl < nfh);
+    float bvec[VEC];
+#pragma unroll
+    for (int t = 0; t < VEC; ++t) bvec[t] = 0.0f;
+    if constexpr (HAS_BIAS) {
+        if (o_ok) {
+#pragma unroll
+            for (int t = 0; t < VEC; ++t)
+                bvec[t] = a.bias[static_cast<int64_t>(f0 + o_fl) * D + o_u * VEC + t];
+        }
+    }
+    const float *o_tbl = tbl + static_cast<size_t>(o_fl) * B * rs + o_u * VEC;
+
+    const int64_t rows = n_end - n_begin;
+    const int64_t n_tiles = (rows + SW - 1) / SW;
+    const int64_t row_elems = static_cast<int64_t>(F) * D;
+
+    for (int64_t t = wave; t < n_tiles; t += kWavesPerBlock) {
+        const int64_t n0 = n_begin + t * SW;
+        const int64_t pn = n0 + p_s;
+        const bool pvalid = p_fok && (pn < n_end);
+        const int64_t pidx = pn * F + f0 + p_fl;
+        const float v = pvalid ? a.x[pidx] : 0.0f;
+        const int k = find_bin(v, e_row, p_n);
+        const float frac = (v - e_row[k]) * iw_row[k];
+        const float qf = quant<Q>(frac);
+        if (pvalid) static_cast<IdxT *>(a.idx)[pidx] = static_cast<IdxT>(k);
+
+        for (int sb = 0; sb < SW; sb += R) {
+            const int s = sb + o_s;
+            const int src = (s * FS + o_fl) & (kWave - 1);
+            const int ks = __shfl(k, src);
+            const float qs = __shfl(qf, src);
+            const int64_t n = n0 + s;
+            if (o_ok && s < SW && n < n_end) {
+                const float *row = o_tbl + static_cast<size_t>(ks) * rs;
+                float r[VEC];
+                if constexpr (VEC == 4) {
+                    const float4 P = *reinterpret_cast<const float4 *>(row);
+                    const float4 W = *reinterpret_cast<const float4 *>(row + D);
+                    r[0] = fmaf(qs, W.x, P.x);
+                    r[1] = fmaf(qs, W.y, P.y);
+                    r[2] = fmaf(qs, W.z, P.z);
+                    r[3] = fmaf(qs, W.w, P.w);
+                } else {
+                    r[0] = fmaf(qs, row[D], row[0]);
+                }
+#pragma unroll
+                for (int t2 = 0; t2 < VEC; ++t2) {
+                    float o = quant<Q>(r[t2]);
+                    if constexpr (HAS_BIAS) o = o + bvec[t2];
+                    r[t2] = o;
+                }
+                store_out<OUT, VEC>(a.out, n * row_elems + static_cast<int64_t>(f0 + o_fl) * D + o_u * VEC, r);
+            }
+        }
+    }
+}
+
+constexpr size_t kLdsBudgetTwoPerCu = 80 * 1024;
+
+int env_int(const char *name, int dflt) {
+    const char *s = getenv(name);
+    if (!s || !*s) return dflt;
+    return atoi(s);
+}
+
+struct FwdPlan {
+    int vec, FS, G, C;
+    int64_t NC;
+    size_t lds;
+};
+
+// FS: the widest power-of-two feature group whose row fits one wave's stores
+// (FS * D/VEC <= 64) and whose tables fit the LDS budget for two workgroups
+// per CU.  Chunks: about 8 workgroups per CU over the grid, a multiple of the
+// XCD count.  PLE_FWD_FS / PLE_FWD_WG_PER_CU override the two choices (tuning).
+bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, bool aligned16, FwdPlan &pl) {
+    pl.vec = (D % 4 == 0 && aligned16) ? 4 : 1;
+    const int U = static_cast<int>(D / pl.vec);
+    if (U > kWave) return false;
+    int fs = 1;
+    while (fs * 2 <= kWave && fs * 2 * U <= kWave && fs < F) fs *= 2;
+    while (fs > 1 && fwd_lds_bytes(fs, static_cast<int>(B), static_cast<int>(D)) > kLdsBudgetTwoPerCu) fs /= 2;
+    const int fs_env = env_int("PLE_FWD_FS", 0);
+    if (fs_env > 0 && (fs_env & (fs_env - 1)) == 0 && fs_env * U <= kWave &&
+        fwd_lds_bytes(fs_env, static_cast<int>(B), static_cast<int>(D)) <= kLdsMax)
+        fs = fs_env;
+    pl.lds = fwd_lds_bytes(fs, static_cast<int>(B), static_cast<int>(D));
+    if (pl.lds > kLdsMax) return false;
+    pl.FS = fs;
+    pl.G = static_cast<int>((F + fs - 1) / fs);
+    const int target = env_int("PLE_FWD_WG_PER_CU", 8) * device_cu_count();
+    int64_t c = (target + pl.G - 1) / pl.G;
+    const int64_t sw = kWave / fs;
+    const int64_t max_c = (N + sw - 1) / sw;          // at least one wave tile per chunk
+    if (c > max_c) c = max_c;
+    if (c < 1) c = 1;
+    c = ((c + kNumXcd - 1) / kNumXcd) * kNumXcd;
+    pl.NC = (N + c - 1) / c;
+    pl.C = static_cast<int>((N + pl.NC - 1) / pl.NC);
+    pl.C = ((pl.C + kNumXcd - 1) / kNumXcd) * kNumXcd;
+    return true;
+}
+
+template <int Q, int OUT, bool HB, int VEC>
+hipError_t launch_idx(const FwdArgs &a, int idxb, dim3 grid, size_t lds, hipStream_t s) {
+    // uint8 indices up to 256 bins, int16 beyond (at most 32766 bins)
+    if (idxb == 1) hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, HB, VEC, uint8_t>), grid, dim3(kBlock), lds, s, a);
+    else hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, HB, VEC, int16_t>), grid, dim3(kBlock), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int Q, int OUT, bool HB>
+hipError_t launch_vec(const FwdArgs &a, int vec, int idxb, dim3 grid, size_t lds, hipStream_t s) {
+    return vec == 4 ? launch_idx<Q, OUT, HB, 4>(a, idxb, grid, lds, s)
+                    : launch_idx<Q, OUT, HB, 1>(a, idxb, grid, lds, s);
+}
+
+// Supported (quant, output) pairs: output == quant without bias (the
+// reference operator), output == F32 with bias (the fused module epilogue).
+template <int Q>
+hipError_t launch_q(const FwdArgs &a, int vec, int idxb, dim3 grid, size_t lds, hipStream_t s) {
+    if (a.bias) return launch_vec<Q, PLE_DTYPE_F32, true>(a, vec, idxb, grid, lds, s);
+    return launch_vec<Q, Q, false>(a, vec, idxb, grid, lds, s);
+}
+
+}  // namespace
+
+int forward_run(const ForwardRequest &r) {
+    if (r.bias ? r.out_dtype != PLE_DTYPE_F32 : r.out_dtype != r.quant) return PLE_E_UNSUPPORTED;
+    const int out_bytes = r.out_dtype == PLE_DTYPE_F32 ? 4 : 2;
+    if (reinterpret_cast<uintptr_t>(r.out) % out_bytes != 0) return PLE_E_MISALIGNED;
+    const bool aligned16 = (reinterpret_cast<uintptr_t>(r.out) % (4 * out_bytes) == 0) &&
+                           (reinterpret_cast<uintptr_t>(r.weight) % 16 == 0);
+    FwdPlan pl;
+    if (!plan_forward(r.N, r.F, r.B, r.D, aligned16, pl)) return PLE_E_UNSUPPORTED;
+    FwdArgs a;
+    a.x = r.x; a.edges = r.edges; a.iw = r.iw; a.nbins = r.nbins; a.weight = r.weight;
+    a.bias = r.bias; a.out = r.out; a.idx = r.idx;
+    a.N = r.N; a.F = static_cast<int>(r.F); a.B = static_cast<int>(r.B); a.D = static_cast<int>(r.D);
+    a.FS = pl.FS; a.G = pl.G; a.C = pl.C; a.NC = pl.NC;
+    const int64_t grid = static_cast<int64_t>(pl.G) * pl.C;
+    if (grid > INT32_MAX) return PLE_E_TOO_LARGE;
+    const int idxb = idx_bytes_for(r.B);
+    hipError_t e;
+    switch (r.quant) {
+        case PLE_DTYPE_F32: e = launch_q<PLE_DTYPE_F32>(a, pl.vec, idxb, dim3(grid), pl.lds, r.stream); break;
+        case PLE_DTYPE_F16: e = launch_q<PLE_DTYPE_F16>(a, pl.vec, idxb, dim3(grid), pl.lds, r.stream); break;
+        default: e = launch_q<PLE_DTYPE_BF16>(a, pl.vec, idxb, dim3(grid), pl.lds, r.stream); break;
+    }
+    return e == hipSuccess ? PLE_OK : static_cast<int>(e);
+}
+
+}  // namespace ple

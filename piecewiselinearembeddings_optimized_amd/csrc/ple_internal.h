@@ -1,0 +1,53 @@
+// Host-side interfaces between the translation units of libple_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/ple_hip.h"
+
+namespace ple {
+
+constexpr size_t kLdsMax = 160 * 1024;   // LDS per workgroup on gfx950
+
+int device_cu_count();
+
+inline int idx_bytes_for(int64_t B) { return B <= 256 ? 1 : (B <= 32768 ? 2 : 4); }
+
+inline bool valid_dtype(int d) { return d == PLE_DTYPE_F32 || d == PLE_DTYPE_F16 || d == PLE_DTYPE_BF16; }
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct ForwardRequest {
+    const float *x, *edges, *iw;
+    const int32_t *nbins;
+    const float *weight, *bias;
+    void *out, *idx;
+    int64_t N, F, B, D;
+    int quant, out_dtype;
+    hipStream_t stream;
+};
+
+// Validated request -> launch.  Returns PLE_OK, PLE_E_* or a hipError_t.
+int forward_run(const ForwardRequest &r);
+
+struct BackwardRequest {
+    const void *g;
+    const float *x, *edges, *iw;
+    const int32_t *nbins;
+    const float *weight;
+    const void *idx;
+    float *dx, *dw, *db;
+    int64_t N, F, B, D;
+    int grad_dtype, quant;
+    void *workspace;
+    size_t workspace_bytes;
+    hipStream_t stream;
+};
+
+size_t backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D);
+int backward_run(const BackwardRequest &r);
+
+}  // namespace ple

@@ -186,3 +186,75 @@ def test_bin_indices_and_outputs_for_special_values(c_oracle):
     same = (got.view(np.uint32) == mirror.view(np.uint32)) | (np.isnan(got) & np.isnan(mirror))
     assert same.all()
     assert (idx[0].cpu().numpy() == w.n_bins - 1).all()       # NaN -> last bin
+
+
+def _random_case(n, f, bmax, d, seed, ragged=True):
+    """Random edges (ragged bin counts up to bmax), x with exact edge hits and
+    out-of-range values, weights and bias."""
+    rng = np.random.default_rng(seed)
+    bins = []
+    for j in range(f):
+        nb = int(rng.integers(1, bmax + 1)) if ragged else bmax
+        if j == 0:
+            nb = bmax
+        e = np.cumsum(rng.uniform(0.05, 1.0, nb + 1)).astype(np.float32) - np.float32(nb * 0.25)
+        bins.append(e)
+    edges, iw, nbins = workloads.pad_bins(bins)
+    x = (rng.standard_normal((n, f)) * 3).astype(np.float32)
+    for j, e in enumerate(bins):
+        hit = rng.random(n) < 0.1
+        x[hit, j] = e[rng.integers(0, e.size, int(hit.sum()))]
+    w = rng.uniform(-0.5, 0.5, (f, edges.shape[1] - 1, d)).astype(np.float32)
+    b = rng.uniform(-0.2, 0.2, (f, d)).astype(np.float32)
+    return workloads.Workload(f"rand{n}x{f}x{bmax}x{d}", x, bins, edges, iw, nbins, w, b)
+
+
+SHAPES = [
+    (1, 1, 1, 1), (7, 3, 5, 10), (129, 5, 7, 15), (1000, 9, 48, 20), (333, 1, 300, 16),
+    (2500, 17, 64, 64), (513, 6, 256, 24), (64, 33, 2, 3), (1025, 4, 130, 2), (700, 2, 1000, 8),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"{n}x{f}x{b}x{d}" for n, f, b, d in SHAPES])
+def test_shape_sweep_forward_and_backward(shape, c_oracle):
+    n, f, bmax, d = shape
+    w = _random_case(n, f, bmax, d, seed=sum(shape))
+    print(f"shape sweep {w.name}", flush=True)
+    x, e, iw, nb, wt, bt = _inputs(w)
+    out, idx = ops.forward_with_bias(x, e, iw, nb, wt, bt, torch.float32)
+    mirror, midx = c_oracle.forward_f32(w.x, w.edges, w.inv_widths, w.n_bins, w.weight, bias=w.bias)
+    np.testing.assert_array_equal(idx.cpu().numpy().astype(np.int32), midx)
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), mirror.view(np.uint32))
+    g = _grad((n, f, d), 5)
+    gx, gw, gb = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, True, True, True)
+    _check_backward(w, "f32", g, gx, gw, gb, c_oracle)
+    # dx alone and dW alone give the same values as together
+    gx2, _, _ = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, True, False, False)
+    _, gw2, gb2 = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, False, True, True)
+    assert torch.equal(gx, gx2) and torch.equal(gw, gw2) and torch.equal(gb, gb2)
+
+
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3])
+def test_fallback_backward_path_matches_oracle(cfg, c_oracle, monkeypatch):
+    """The simple (non-fused) backward kernels, forced by PLE_BWD_SIMPLE=1."""
+    monkeypatch.setenv("PLE_BWD_SIMPLE", "1")
+    w = workloads.make(cfg, min(REDUCED[cfg] or 4096, 4096))
+    n, f, bmax, d = w.shape
+    print(f"fallback backward {w.name} shape={w.shape}", flush=True)
+    x, e, iw, nb, wt, bt = _inputs(w)
+    _, idx = ops.forward_with_bias(x, e, iw, nb, wt, bt, torch.float32)
+    g = _grad((n, f, d), 200 + cfg)
+    gx, gw, gb = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, True, True, True)
+    _check_backward(w, "f32", g, gx, gw, gb, c_oracle)
+
+
+def test_empty_batch():
+    w = workloads.make(0)
+    x, e, iw, nb, wt, bt = _inputs(w)
+    x0 = x[:0].contiguous()
+    out, idx = ops.forward_with_bias(x0, e, iw, nb, wt, bt, torch.float32)
+    assert out.shape == (0, x.shape[1], wt.shape[2]) and idx.shape == (0, x.shape[1])
+    g = torch.zeros((0, x.shape[1], wt.shape[2]), device=DEV)
+    gx, gw, gb = ops.backward_with_bias(g, x0, e, iw, nb, wt, idx, torch.float32, True, True, True)
+    assert gx.shape == (0, x.shape[1])
+    assert torch.count_nonzero(gw) == 0 and torch.count_nonzero(gb) == 0
