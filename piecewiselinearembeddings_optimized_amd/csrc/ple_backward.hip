@@ -56,7 +56,7 @@ struct BwdArgs {
     int Cd;          // chunks holding samples (the ones that write partials)
     int64_t NC;      // samples per chunk
     // fused path
-    int FS, G, NT, P, LGW, nbits;
+    int FS, G, NT, P, LGW, nbits;   // P: pairs per sub-tile (kP)
     int o_qw, o_hist, o_db, o_edge, o_iw, o_nb, o_info, o_order, o_rank, o_cnt, o_seg, o_dx, o_rec,
         o_rkey, o_rfl, o_tmp;
 };
@@ -89,10 +89,14 @@ __device__ void block_exclusive_scan(int *a, int n, int *tmp) {
     __syncthreads();
 }
 
-template <int GD, int Q, int VEC, typename IdxT>
+constexpr int kP = 1024;                        // (sample, feature) pairs per sub-tile
+constexpr int kPairsPerThread = kP / kBlock;
+constexpr int kUB = 8;                          // sorted rows per prefetch batch (phase F)
+
+template <int GD, int Q, int VEC, int LGW_T, typename IdxT>
 __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
     extern __shared__ __align__(16) unsigned char lds[];
-    const int FS = a.FS, B = a.B, D = a.D, F = a.F, NT = a.NT, P = a.P;
+    const int FS = a.FS, B = a.B, D = a.D, F = a.F, NT = a.NT;
     const int KB = B + 1;                   // keys per feature; key B marks padding rows
     float *s_qw = reinterpret_cast<float *>(lds + a.o_qw);        // [FS][B][D]
     float *s_hist = reinterpret_cast<float *>(lds + a.o_hist);    // [FS][B][2D]
@@ -122,6 +126,26 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
     const int wave = tid / kWave;
     const int lane = tid % kWave;
 
+    // pair inputs of a sub-tile, prefetched into registers one sub-tile ahead:
+    // thread -> pairs i = tid + u * kBlock, i -> (sample i / FS, feature i % FS)
+    int pk[kPairsPerThread];
+    float pv[kPairsPerThread];
+    auto fetch_pairs = [&](int64_t sub) __attribute__((always_inline)) {
+        const int64_t ns = min(static_cast<int64_t>(NT), n_end - sub);
+#pragma unroll
+        for (int u = 0; u < kPairsPerThread; ++u) {
+            const int i = tid + u * kBlock;
+            const int s = i / FS;
+            const int fl = i - s * FS;
+            // unconditional loads (pair 0 stands in for padding) keep the
+            // wait for them a single counted one
+            const int64_t pair = (s < ns && fl < nfh) ? (sub + s) * F + f0 + fl : 0;
+            pk[u] = load_idx<IdxT>(a.idx, pair);
+            pv[u] = a.x[pair];
+        }
+    };
+    fetch_pairs(n_begin);
+
     // ---- stage tables, clear accumulators ---------------------------------
     for (int i = tid; i < FS; i += kBlock) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
     for (int i = tid; i < FS * KB; i += kBlock) {
@@ -149,29 +173,30 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
     }
     __syncthreads();
 
-    const int lgw = a.LGW;                 // lanes per grad_output row (power of two)
-    const int LG = kBlock / lgw;           // lane groups (slices) per workgroup
+    const int lgw = LGW_T > 0 ? LGW_T : a.LGW;   // lanes per grad_output row (power of two)
+    const int LG = kBlock / lgw;                  // lane groups (slices) per workgroup
     const int lg = tid / lgw;
     const int lc = tid - lg * lgw;
     const bool c_ok = lc < D / VEC;
-    const int R = P / LG;                  // sorted rows per slice
-    const int NB = P / kWave;              // 64-pair blocks per sub-tile
-    const int NBf = NT / kWave;            // blocks per feature
+    const int R = kP / LG;                        // sorted rows per slice
+    const int NB = kP / kWave;                    // 64-pair blocks per sub-tile
+    const int NBf = NT / kWave;                   // blocks per feature
     const int D2 = 2 * D, D3 = 3 * D;
 
     for (int64_t sub = n_begin; sub < n_end; sub += NT) {
         const int ns = static_cast<int>(min(static_cast<int64_t>(NT), n_end - sub));
 
         // A. pair info, stored feature-major (p = fl * NT + s)
-        for (int i = tid; i < P; i += kBlock) {
+#pragma unroll
+        for (int u = 0; u < kPairsPerThread; ++u) {
+            const int i = tid + u * kBlock;
             const int s = i / FS;
             const int fl = i - s * FS;
             int key = B;
             float qf = 0.0f;
             if (s < ns && fl < nfh) {
-                const int64_t pair = (sub + s) * F + f0 + fl;
-                const int k = clamp_bin(load_idx<IdxT>(a.idx, pair), s_nb[fl]);
-                const float v = a.x[pair];
+                const int k = clamp_bin(pk[u], s_nb[fl]);
+                const float v = pv[u];
                 const float e = s_edge[fl * KB + k];
                 qf = quant<Q>((v - e) * s_iw[fl * B + k]);
                 key = k | ((k > 0 && v == e) ? 0x8000 : 0);
@@ -215,7 +240,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
         block_exclusive_scan(s_seg, FS * KB, s_tmp);
 
         // D. scatter: sorted position -> sample
-        for (int p = tid; p < P; p += kBlock) {
+        for (int p = tid; p < kP; p += kBlock) {
             const int fl = p / NT;
             const int s = p - fl * NT;
             const int k = __float_as_int(s_info[p].y) & 0x7fff;
@@ -224,9 +249,11 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
         }
         __syncthreads();
 
-        // F. slices of sorted rows
+        // the next sub-tile's pair inputs travel while this one is reduced
+        if (sub + NT < n_end) fetch_pairs(sub + NT);
+
+        // F. slices of sorted rows, gradient rows prefetched a batch ahead
         {
-            constexpr int UB = 8;
             int cur = -1, cur_fl = -1;
             bool first_key = true, first_fl = true;
             float ab[VEC], aw[VEC], ad[VEC];
@@ -237,104 +264,9 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
                 s_rfl[lg] = -1;
             }
             float *rec = s_rec + lg * D3 + lc * VEC;
-            const int r0 = lg * R;
-            for (int rb = r0; rb < r0 + R; rb += UB) {
-                int sv[UB], kbv[UB], flv[UB];
-                float qfv[UB], gv[UB][VEC];
-#pragma unroll
-                for (int u = 0; u < UB; ++u) {
-                    const int r = rb + u;
-                    const int fl = r / NT;
-                    const int s = s_order[r];
-                    const float2 inf = s_info[fl * NT + s];
-                    sv[u] = s;
-                    flv[u] = fl;
-                    kbv[u] = __float_as_int(inf.y);
-                    qfv[u] = inf.x;
-#pragma unroll
-                    for (int t = 0; t < VEC; ++t) gv[u][t] = 0.0f;
-                    if (c_ok && (kbv[u] & 0x7fff) < B)
-                        load_grad_vec<GD, VEC>(a.g, ((sub + s) * F + f0 + fl) * D + lc * VEC, gv[u]);
-                }
-#pragma unroll
-                for (int u = 0; u < UB; ++u) {
-                    const int k = kbv[u] & 0x7fff;
-                    if (k >= B) continue;                  // padding row (whole slice agrees)
-                    const int fl = flv[u];
-                    const int kk = fl * KB + k;
-                    if (kk != cur) {
-                        if (cur >= 0) {
-                            if (first_key) {
-                                if (c_ok) {
-#pragma unroll
-                                    for (int t = 0; t < VEC; ++t) {
-                                        rec[t] = ab[t];
-                                        rec[D + t] = aw[t];
-                                    }
-                                }
-                                if (lc == 0) s_rkey[lg] = cur;
-                                first_key = false;
-                            } else if (c_ok) {
-                                const int cfl = cur / KB;
-                                float *h = s_hist + (static_cast<size_t>(cfl) * B + (cur - cfl * KB)) * D2 + lc * VEC;
-#pragma unroll
-                                for (int t = 0; t < VEC; ++t) {
-                                    h[t] += ab[t];
-                                    h[D + t] += aw[t];
-                                }
-                            }
-                        }
-#pragma unroll
-                        for (int t = 0; t < VEC; ++t) ab[t] = aw[t] = 0.0f;
-                        cur = kk;
-                    }
-                    if (fl != cur_fl) {
-                        if (cur_fl >= 0) {
-                            if (first_fl) {
-                                if (c_ok) {
-#pragma unroll
-                                    for (int t = 0; t < VEC; ++t) rec[D2 + t] = ad[t];
-                                }
-                                if (lc == 0) s_rfl[lg] = cur_fl;
-                                first_fl = false;
-                            } else if (c_ok) {
-#pragma unroll
-                                for (int t = 0; t < VEC; ++t) s_db[cur_fl * D + lc * VEC + t] += ad[t];
-                            }
-                        }
-#pragma unroll
-                        for (int t = 0; t < VEC; ++t) ad[t] = 0.0f;
-                        cur_fl = fl;
-                    }
-                    const bool edge = (kbv[u] & 0x8000) != 0;
-                    const float *wrow = s_qw + (static_cast<size_t>(fl) * B + k) * D + lc * VEC;
-                    float dot = 0.0f, dot2 = 0.0f;
-#pragma unroll
-                    for (int t = 0; t < VEC; ++t) {
-                        const float gr = gv[u][t];
-                        const float gq = quant<Q>(gr);
-                        ab[t] += gq;
-                        aw[t] = fmaf(qfv[u], gq, aw[t]);
-                        ad[t] += gr;
-                        if (c_ok) dot = fmaf(gq, wrow[t], dot);
-                    }
-                    if (edge && c_ok) {
-#pragma unroll
-                        for (int t = 0; t < VEC; ++t) dot2 = fmaf(quant<Q>(gv[u][t]), (wrow - D)[t], dot2);
-                    }
-                    for (int off = lgw >> 1; off > 0; off >>= 1) {
-                        dot += __shfl_xor(dot, off, lgw);
-                        dot2 += __shfl_xor(dot2, off, lgw);
-                    }
-                    if (lc == 0) {
-                        float r = dot * s_iw[fl * B + k];
-                        if (edge) r = fmaf(dot2, s_iw[fl * B + k - 1], r);
-                        s_dx[fl * NT + sv[u]] = r;
-                    }
-                }
-            }
-            // the slice's last key and feature
-            if (cur >= 0) {
+
+            auto flush_key = [&]() __attribute__((always_inline)) {
+                if (cur < 0) return;
                 if (first_key) {
                     if (c_ok) {
 #pragma unroll
@@ -344,6 +276,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
                         }
                     }
                     if (lc == 0) s_rkey[lg] = cur;
+                    first_key = false;
                 } else if (c_ok) {
                     const int cfl = cur / KB;
                     float *h = s_hist + (static_cast<size_t>(cfl) * B + (cur - cfl * KB)) * D2 + lc * VEC;
@@ -353,19 +286,124 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
                         h[D + t] += aw[t];
                     }
                 }
-            }
-            if (cur_fl >= 0) {
+            };
+            auto flush_fl = [&]() __attribute__((always_inline)) {
+                if (cur_fl < 0) return;
                 if (first_fl) {
                     if (c_ok) {
 #pragma unroll
                         for (int t = 0; t < VEC; ++t) rec[D2 + t] = ad[t];
                     }
                     if (lc == 0) s_rfl[lg] = cur_fl;
+                    first_fl = false;
                 } else if (c_ok) {
 #pragma unroll
                     for (int t = 0; t < VEC; ++t) s_db[cur_fl * D + lc * VEC + t] += ad[t];
                 }
+            };
+
+            // sorted position r -> (feature r / NT, sample s_order[r]); NT is a
+            // power of two
+            const int nt_shift = __ffs(NT) - 1;
+            float gA[kUB][VEC], gB[kUB][VEC];
+
+            auto issue = [&](int rb, float (&gv)[kUB][VEC]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int u = 0; u < kUB; ++u) {
+                    const int r = rb + u;
+                    const int fl = r >> nt_shift;
+                    const int s = s_order[r];
+                    const int kb = __float_as_int(s_info[(fl << nt_shift) + s].y);
+                    // every lane loads: a padding row or an idle lane reads element 0,
+                    // which process() never uses (padding rows are skipped, idle
+                    // lanes' sums are never stored).  With no branch around the
+                    // loads, the compiler waits for each batch separately.
+                    const bool ok = c_ok && (kb & 0x7fff) < B;
+                    const int64_t at = ok ? ((sub + s) * F + f0 + fl) * D + lc * VEC : 0;
+                    load_grad_vec<GD, VEC>(a.g, at, gv[u]);
+                }
+            };
+
+            // Per row, all LDS reads are unconditional and the arithmetic is
+            // masked rather than branched; the only branch is the (rare)
+            // change of key.  Idle lanes read column 0 and contribute 0.
+            const int lcx = c_ok ? lc : 0;
+            auto process = [&](int rb, const float (&gv)[kUB][VEC]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int u = 0; u < kUB; ++u) {
+                    const int r = rb + u;
+                    const int fl = r >> nt_shift;
+                    const int s = s_order[r];
+                    const int p = (fl << nt_shift) + s;
+                    const float2 inf = s_info[p];
+                    const int kb = __float_as_int(inf.y);
+                    const int k = kb & 0x7fff;
+                    const bool valid = k < B;               // padding rows sort last
+                    const int kv = valid ? k : 0;
+                    const int km = kv > 0 ? kv - 1 : 0;
+                    const bool edge = (kb & 0x8000) != 0;  // only set for k >= 1
+                    const float *wrow = s_qw + (static_cast<size_t>(fl) * B + kv) * D + lcx * VEC;
+                    const float *wprv = s_qw + (static_cast<size_t>(fl) * B + km) * D + lcx * VEC;
+                    float w[VEC], wp[VEC];
+                    if constexpr (VEC == 4) {
+                        const float4 a4 = *reinterpret_cast<const float4 *>(wrow);
+                        const float4 b4 = *reinterpret_cast<const float4 *>(wprv);
+                        w[0] = a4.x; w[1] = a4.y; w[2] = a4.z; w[3] = a4.w;
+                        wp[0] = b4.x; wp[1] = b4.y; wp[2] = b4.z; wp[3] = b4.w;
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < VEC; ++t) {
+                            w[t] = wrow[t];
+                            wp[t] = wprv[t];
+                        }
+                    }
+                    const float iwk = s_iw[fl * B + kv];
+                    const float iwp = s_iw[fl * B + km];
+                    const int kk = fl * KB + k;
+                    if (valid && kk != cur) {
+                        flush_key();
+#pragma unroll
+                        for (int t = 0; t < VEC; ++t) ab[t] = aw[t] = 0.0f;
+                        cur = kk;
+                        if (fl != cur_fl) {
+                            flush_fl();
+#pragma unroll
+                            for (int t = 0; t < VEC; ++t) ad[t] = 0.0f;
+                            cur_fl = fl;
+                        }
+                    }
+                    float dot = 0.0f, dot2 = 0.0f;
+#pragma unroll
+                    for (int t = 0; t < VEC; ++t) {
+                        const float gr = gv[u][t];
+                        const float gq = quant<Q>(gr);
+                        const float m = valid ? gq : 0.0f;
+                        ab[t] += m;
+                        aw[t] = fmaf(inf.x, m, aw[t]);
+                        ad[t] += valid ? gr : 0.0f;
+                        dot = fmaf(gq, w[t], dot);
+                        dot2 = fmaf(gq, wp[t], dot2);
+                    }
+                    float part = dot * iwk;
+                    part = edge ? fmaf(dot2, iwp, part) : part;
+                    part = c_ok ? part : 0.0f;
+                    if constexpr (LGW_T > 0) part = group_sum<LGW_T>(part);
+                    else part = group_sum_rt(part, lgw);
+                    if (lc == 0 && valid) s_dx[p] = part;
+                }
+            };
+
+            const int r0 = lg * R;
+            const int r1 = r0 + R;
+            issue(r0, gA);
+            for (int rb = r0; rb < r1; rb += 2 * kUB) {
+                if (rb + kUB < r1) issue(rb + kUB, gB);
+                process(rb, gA);
+                if (rb + 2 * kUB < r1) issue(rb + 2 * kUB, gA);
+                if (rb + kUB < r1) process(rb + kUB, gB);
             }
+            flush_key();
+            flush_fl();
         }
         __syncthreads();
 
@@ -409,7 +447,9 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
 
         // H. dx, coalesced along the group's features
         if (a.dx) {
-            for (int i = tid; i < P; i += kBlock) {
+#pragma unroll
+            for (int u = 0; u < kPairsPerThread; ++u) {
+                const int i = tid + u * kBlock;
                 const int s = i / FS;
                 const int fl = i - s * FS;
                 if (s < ns && fl < nfh) a.dx[(sub + s) * F + f0 + fl] = s_dx[fl * NT + s];
@@ -647,23 +687,22 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, int g_align) {
     BwdPlan pl{};
     const int cus = device_cu_count();
     pl.fused = false;
-    // fused geometry
+    // fused geometry: VEC=4 rows of D/4 lanes when D allows, else one column
+    // per lane; lane groups of a power-of-two width between 2 and 64
     if (B <= 4096 && env_int("PLE_BWD_SIMPLE", 0) == 0) {
-        const int vec = (D % 4 == 0 && g_align >= 4) ? 4 : ((D % 2 == 0 && g_align >= 2) ? 2 : 1);
+        const int vec = (D % 4 == 0 && D >= 8 && g_align >= 4) ? 4 : 1;
         const int uv = static_cast<int>(D / vec);
-        int lgw = 1;
+        int lgw = 2;
         while (lgw < uv) lgw *= 2;
         if (lgw <= kWave) {
             const int LG = kBlock / lgw;
-            const int P = env_int("PLE_BWD_P", 1024);
             int best_fs = 0;
             size_t best_lds = 0;
             BwdArgs geo{};
             for (int fs = 4; fs >= 1; fs /= 2) {
-                if (P / fs < kWave || (P / fs) % kWave != 0 || (fs > 1 && fs > F)) continue;
-                if (P % LG != 0 || (P / LG) % 8 != 0) continue;
+                if (fs > 1 && fs > F) continue;
                 BwdArgs t{};
-                const size_t lds = fused_layout(t, fs, P, static_cast<int>(B), static_cast<int>(D), LG);
+                const size_t lds = fused_layout(t, fs, kP, static_cast<int>(B), static_cast<int>(D), LG);
                 if (lds <= kFusedLdsTwoPerCu || (fs == 1 && lds <= kLdsMax)) {
                     best_fs = fs;
                     best_lds = lds;
@@ -672,10 +711,10 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, int g_align) {
                 }
             }
             const int fs_env = env_int("PLE_BWD_FS", 0);
-            if (fs_env == 1 || fs_env == 2 || fs_env == 4 || fs_env == 8) {
+            if (fs_env == 1 || fs_env == 2 || fs_env == 4 || fs_env == 8 || fs_env == 16) {
                 BwdArgs t{};
-                const size_t lds = fused_layout(t, fs_env, P, static_cast<int>(B), static_cast<int>(D), LG);
-                if (lds <= kLdsMax && P / fs_env >= kWave && (P / fs_env) % kWave == 0) {
+                const size_t lds = fused_layout(t, fs_env, kP, static_cast<int>(B), static_cast<int>(D), LG);
+                if (lds <= kLdsMax) {
                     best_fs = fs_env;
                     best_lds = lds;
                     geo = t;
@@ -687,8 +726,8 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, int g_align) {
                 pl.lds = best_lds;
                 geo.FS = best_fs;
                 geo.G = static_cast<int>((F + best_fs - 1) / best_fs);
-                geo.P = P;
-                geo.NT = P / best_fs;
+                geo.P = kP;
+                geo.NT = kP / best_fs;
                 geo.LGW = lgw;
                 int nbits = 0;
                 while ((1ll << nbits) <= B) ++nbits;      // keys 0..B
@@ -730,11 +769,26 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, int g_align) {
 
 // Bin indices are uint8 (up to 256 bins) or int16 (up to 32766 bins, the
 // largest key the fused sort encodes).
-template <int GD, int Q, int VEC>
+template <int GD, int Q, int VEC, int LGW>
 hipError_t launch_fused_idx(const BwdArgs &a, int idxb, dim3 grid, size_t lds, hipStream_t s) {
-    if (idxb == 1) hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, VEC, uint8_t>), grid, dim3(kBlock), lds, s, a);
-    else hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, VEC, int16_t>), grid, dim3(kBlock), lds, s, a);
+    if (idxb == 1) hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, VEC, LGW, uint8_t>), grid, dim3(kBlock), lds, s, a);
+    else hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, VEC, LGW, int16_t>), grid, dim3(kBlock), lds, s, a);
     return hipGetLastError();
+}
+
+// Lane-group width as a template argument for the VEC=4 rows (DPP
+// reductions); the one-column-per-lane variant takes it at run time.
+template <int GD, int Q>
+hipError_t launch_fused(const BwdArgs &a, int vec, int idxb, dim3 grid, size_t lds, hipStream_t s) {
+    if (vec == 4) {
+        switch (a.LGW) {
+            case 2: return launch_fused_idx<GD, Q, 4, 2>(a, idxb, grid, lds, s);
+            case 4: return launch_fused_idx<GD, Q, 4, 4>(a, idxb, grid, lds, s);
+            case 8: return launch_fused_idx<GD, Q, 4, 8>(a, idxb, grid, lds, s);
+            default: return launch_fused_idx<GD, Q, 4, 16>(a, idxb, grid, lds, s);
+        }
+    }
+    return launch_fused_idx<GD, Q, 1, 0>(a, idxb, grid, lds, s);
 }
 
 template <int GD, int Q>
@@ -742,11 +796,7 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
     hipError_t e = hipSuccess;
     if (pl.fused) {
         const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.G) * pl.C));
-        switch (pl.vec) {
-            case 4: e = launch_fused_idx<GD, Q, 4>(a, idxb, grid, pl.lds, s); break;
-            case 2: e = launch_fused_idx<GD, Q, 2>(a, idxb, grid, pl.lds, s); break;
-            default: e = launch_fused_idx<GD, Q, 1>(a, idxb, grid, pl.lds, s); break;
-        }
+        e = launch_fused<GD, Q>(a, pl.vec, idxb, grid, pl.lds, s);
         if (e != hipSuccess) return e;
     } else {
         if (want_dx) {

@@ -119,6 +119,37 @@ __device__ __forceinline__ void store_out(void *base, int64_t i, const float *v)
 }
 
 // ---------------------------------------------------------------------------
+// lane-group reductions
+// ---------------------------------------------------------------------------
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of W lanes (W a power of two); every lane of the
+// group receives the sum.  Groups of up to 16 lanes reduce with DPP inside a
+// 16-lane row (quad permutes, then half-row and row mirrors); wider groups
+// finish with cross-row shuffles.  All lanes of a group must be active.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "group width must be a power of two");
+    if constexpr (W >= 2) v += dpp_f32<0xB1>(v);    // quad_perm [1,0,3,2]
+    if constexpr (W >= 4) v += dpp_f32<0x4E>(v);    // quad_perm [2,3,0,1]
+    if constexpr (W >= 8) v += dpp_f32<0x141>(v);   // row_half_mirror
+    if constexpr (W >= 16) v += dpp_f32<0x140>(v);  // row_mirror
+    if constexpr (W >= 32) v += __shfl_xor(v, 16);
+    if constexpr (W >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+// Same, for a group width known only at run time (power of two <= 64).
+__device__ __forceinline__ float group_sum_rt(float v, int w) {
+    for (int off = w >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, w);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
 // bins
 // ---------------------------------------------------------------------------
 
