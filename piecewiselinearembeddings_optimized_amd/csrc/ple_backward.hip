@@ -55,11 +55,17 @@ struct BwdArgs {
     int C;           // chunks in the grid (fused: a multiple of kNumXcd)
     int Cd;          // chunks holding samples (the ones that write partials)
     int64_t NC;      // samples per chunk
+    int db_from_buckets;   // finalize: db = sum of the bin buckets (no raw-gradient partials)
     // fused path
     int FS, G, NT, P, LGW, nbits;   // P: pairs per sub-tile (kP)
     int o_qw, o_hist, o_db, o_edge, o_iw, o_nb, o_info, o_order, o_rank, o_cnt, o_seg, o_dx, o_rec,
         o_rkey, o_rfl, o_tmp;
 };
+
+// A row of zeros in device memory: padding rows and idle lanes of the fused
+// kernel load from here, so their contributions are exact zeros without any
+// masking in the row loop.  Never written.
+__device__ __attribute__((aligned(16))) float g_zero_row[64] = {};
 
 // Exclusive prefix sum of a[0..n) in place, all kBlock threads.
 __device__ void block_exclusive_scan(int *a, int n, int *tmp) {
@@ -91,10 +97,15 @@ __device__ void block_exclusive_scan(int *a, int n, int *tmp) {
 
 constexpr int kP = 1024;                        // (sample, feature) pairs per sub-tile
 constexpr int kPairsPerThread = kP / kBlock;
-constexpr int kUB = 8;                          // sorted rows per prefetch batch (phase F)
+constexpr int kRowRegs = 32;                    // gradient floats per lane in one prefetch batch (phase F)
 
 template <int GD, int Q, int VEC, int LGW_T, typename IdxT>
 __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
+    constexpr int kUB = VEC == 8 ? kRowRegs / 8 : 8;   // sorted rows per prefetch batch
+    // With fp32 rounding the bias gradient is the sum of the bin buckets
+    // (taken at finalize); otherwise it needs its own sum of the unrounded
+    // gradient.
+    constexpr bool kRawDb = Q != PLE_DTYPE_F32;
     extern __shared__ __align__(16) unsigned char lds[];
     const int FS = a.FS, B = a.B, D = a.D, F = a.F, NT = a.NT;
     const int KB = B + 1;                   // keys per feature; key B marks padding rows
@@ -105,7 +116,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
     float *s_iw = reinterpret_cast<float *>(lds + a.o_iw);        // [FS][B]
     int *s_nb = reinterpret_cast<int *>(lds + a.o_nb);            // [FS]
     float2 *s_info = reinterpret_cast<float2 *>(lds + a.o_info);  // [P] {q(frac), key|edge}
-    uint16_t *s_order = reinterpret_cast<uint16_t *>(lds + a.o_order);  // [P] sorted -> sample
+    uint2 *s_sdesc = reinterpret_cast<uint2 *>(lds + a.o_order);        // [P] sorted rows {q(frac), key|edge|s<<16}
     uint8_t *s_rank = reinterpret_cast<uint8_t *>(lds + a.o_rank);      // [P]
     uint16_t *s_cnt = reinterpret_cast<uint16_t *>(lds + a.o_cnt);      // [P/64][B+1]
     int *s_seg = reinterpret_cast<int *>(lds + a.o_seg);                // [FS*(B+1)]
@@ -239,13 +250,16 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
         __syncthreads();
         block_exclusive_scan(s_seg, FS * KB, s_tmp);
 
-        // D. scatter: sorted position -> sample
+        // D. scatter: sorted position -> row descriptor {q(frac), key | edge | sample << 16}
         for (int p = tid; p < kP; p += kBlock) {
             const int fl = p / NT;
             const int s = p - fl * NT;
-            const int k = __float_as_int(s_info[p].y) & 0x7fff;
+            const float2 inf = s_info[p];
+            const int kb = __float_as_int(inf.y);
+            const int k = kb & 0x7fff;
             const int slot = s_seg[fl * KB + k] + s_cnt[(p / kWave) * KB + k] + s_rank[p];
-            s_order[slot] = static_cast<uint16_t>(s);
+            s_sdesc[slot] = make_uint2(__float_as_uint(inf.x), static_cast<uint32_t>(kb & 0xffff) |
+                                                                (static_cast<uint32_t>(s) << 16));
         }
         __syncthreads();
 
@@ -254,7 +268,11 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
 
         // F. slices of sorted rows, gradient rows prefetched a batch ahead
         {
-            int cur = -1, cur_fl = -1;
+            // Running sums of the slice's current key (feature, bin) -- packed as
+            // fl << 16 | k -- and, with rounding quantisation, of its feature.
+            // Padding rows (key B) and idle lanes (lc >= D / VEC) read a row of
+            // zeros, so they add nothing and need no masking.
+            int cur = -1, db_fl = -1;
             bool first_key = true, first_fl = true;
             float ab[VEC], aw[VEC], ad[VEC];
 #pragma unroll
@@ -265,145 +283,154 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
             }
             float *rec = s_rec + lg * D3 + lc * VEC;
 
+            // first key of the slice -> record; later keys -> straight into the
+            // histogram (this slice is their only writer).  One read-modify-write
+            // through a selected pointer keeps the code inlined per row small.
             auto flush_key = [&]() __attribute__((always_inline)) {
-                if (cur < 0) return;
-                if (first_key) {
-                    if (c_ok) {
-#pragma unroll
-                        for (int t = 0; t < VEC; ++t) {
-                            rec[t] = ab[t];
-                            rec[D + t] = aw[t];
-                        }
-                    }
-                    if (lc == 0) s_rkey[lg] = cur;
-                    first_key = false;
-                } else if (c_ok) {
-                    const int cfl = cur / KB;
-                    float *h = s_hist + (static_cast<size_t>(cfl) * B + (cur - cfl * KB)) * D2 + lc * VEC;
+                if (cur < 0 || (cur & 0xffff) >= B) return;
+                float *h = s_hist + (static_cast<size_t>(cur >> 16) * B + (cur & 0xffff)) * D2 + lc * VEC;
+                float *dst = first_key ? rec : h;
+                if (c_ok) {
+                    float ob[VEC], ow[VEC];
+                    lds_load_vec<VEC>(dst, ob);
+                    lds_load_vec<VEC>(dst + D, ow);
 #pragma unroll
                     for (int t = 0; t < VEC; ++t) {
-                        h[t] += ab[t];
-                        h[D + t] += aw[t];
+                        ob[t] = first_key ? ab[t] : ob[t] + ab[t];
+                        ow[t] = first_key ? aw[t] : ow[t] + aw[t];
                     }
+                    lds_store_vec<VEC>(dst, ob);
+                    lds_store_vec<VEC>(dst + D, ow);
                 }
+                if (first_key && lc == 0) s_rkey[lg] = cur;
+                first_key = false;
             };
             auto flush_fl = [&]() __attribute__((always_inline)) {
-                if (cur_fl < 0) return;
-                if (first_fl) {
-                    if (c_ok) {
+                if (db_fl < 0) return;
+                float *dst = first_fl ? rec + D2 : s_db + db_fl * D + lc * VEC;
+                if (c_ok) {
+                    float o[VEC];
+                    lds_load_vec<VEC>(dst, o);
 #pragma unroll
-                        for (int t = 0; t < VEC; ++t) rec[D2 + t] = ad[t];
-                    }
-                    if (lc == 0) s_rfl[lg] = cur_fl;
-                    first_fl = false;
-                } else if (c_ok) {
-#pragma unroll
-                    for (int t = 0; t < VEC; ++t) s_db[cur_fl * D + lc * VEC + t] += ad[t];
+                    for (int t = 0; t < VEC; ++t) o[t] = first_fl ? ad[t] : o[t] + ad[t];
+                    lds_store_vec<VEC>(dst, o);
                 }
+                if (first_fl && lc == 0) s_rfl[lg] = db_fl;
+                first_fl = false;
             };
 
-            // sorted position r -> (feature r / NT, sample s_order[r]); NT is a
-            // power of two
+            // sorted position r -> feature r / NT (NT is a power of two)
             const int nt_shift = __ffs(NT) - 1;
             float gA[kUB][VEC], gB[kUB][VEC];
+
+            // gradient rows of this sub-tile: 32-bit element offsets from the
+            // sub-tile's first pair (the planner keeps NT * F * D below 2^31)
+            const char *gsub = static_cast<const char *>(a.g) +
+                               ((sub * F + f0) * D) * static_cast<int64_t>(GD == PLE_DTYPE_F32 ? 4 : 2);
+            const int rowF = F * D;
 
             auto issue = [&](int rb, float (&gv)[kUB][VEC]) __attribute__((always_inline)) {
 #pragma unroll
                 for (int u = 0; u < kUB; ++u) {
                     const int r = rb + u;
                     const int fl = r >> nt_shift;
-                    const int s = s_order[r];
-                    const int kb = __float_as_int(s_info[(fl << nt_shift) + s].y);
-                    // every lane loads: a padding row or an idle lane reads element 0,
-                    // which process() never uses (padding rows are skipped, idle
-                    // lanes' sums are never stored).  With no branch around the
-                    // loads, the compiler waits for each batch separately.
-                    const bool ok = c_ok && (kb & 0x7fff) < B;
-                    const int64_t at = ok ? ((sub + s) * F + f0 + fl) * D + lc * VEC : 0;
-                    load_grad_vec<GD, VEC>(a.g, at, gv[u]);
+                    const uint32_t dw = s_sdesc[r].y;
+                    const int s = static_cast<int>(dw >> 16);
+                    // every lane loads, with no branch around the load (so the
+                    // compiler waits for each batch separately); padding rows
+                    // and idle lanes load zeros
+                    const bool ok = c_ok && static_cast<int>(dw & 0x7fff) < B;
+                    const void *src = ok ? static_cast<const void *>(gsub) : static_cast<const void *>(g_zero_row);
+                    const int at = ok ? s * rowF + fl * D + lc * VEC : 0;
+                    load_grad_vec<GD, VEC>(src, at, gv[u]);   // 16-bit zeros decode to +0 too
                 }
             };
 
-            // Per row, all LDS reads are unconditional and the arithmetic is
-            // masked rather than branched; the only branch is the (rare)
-            // change of key.  Idle lanes read column 0 and contribute 0.
+            // weight row and inverse width of the current key, reloaded from LDS
+            // when the key changes (idle lanes read column 0; their g is 0)
             const int lcx = c_ok ? lc : 0;
+            float wk[VEC];
+            float iwk = 0.0f;
+#pragma unroll
+            for (int t = 0; t < VEC; ++t) wk[t] = 0.0f;
             auto process = [&](int rb, const float (&gv)[kUB][VEC]) __attribute__((always_inline)) {
+                uint2 dsc[kUB];
+#pragma unroll
+                for (int u = 0; u < kUB; ++u) dsc[u] = s_sdesc[rb + u];
 #pragma unroll
                 for (int u = 0; u < kUB; ++u) {
                     const int r = rb + u;
                     const int fl = r >> nt_shift;
-                    const int s = s_order[r];
-                    const int p = (fl << nt_shift) + s;
-                    const float2 inf = s_info[p];
-                    const int kb = __float_as_int(inf.y);
-                    const int k = kb & 0x7fff;
-                    const bool valid = k < B;               // padding rows sort last
-                    const int kv = valid ? k : 0;
-                    const int km = kv > 0 ? kv - 1 : 0;
-                    const bool edge = (kb & 0x8000) != 0;  // only set for k >= 1
-                    const float *wrow = s_qw + (static_cast<size_t>(fl) * B + kv) * D + lcx * VEC;
-                    const float *wprv = s_qw + (static_cast<size_t>(fl) * B + km) * D + lcx * VEC;
-                    float w[VEC], wp[VEC];
-                    if constexpr (VEC == 4) {
-                        const float4 a4 = *reinterpret_cast<const float4 *>(wrow);
-                        const float4 b4 = *reinterpret_cast<const float4 *>(wprv);
-                        w[0] = a4.x; w[1] = a4.y; w[2] = a4.z; w[3] = a4.w;
-                        wp[0] = b4.x; wp[1] = b4.y; wp[2] = b4.z; wp[3] = b4.w;
-                    } else {
-#pragma unroll
-                        for (int t = 0; t < VEC; ++t) {
-                            w[t] = wrow[t];
-                            wp[t] = wprv[t];
-                        }
-                    }
-                    const float iwk = s_iw[fl * B + kv];
-                    const float iwp = s_iw[fl * B + km];
-                    const int kk = fl * KB + k;
-                    if (valid && kk != cur) {
+                    const float qf = __uint_as_float(dsc[u].x);
+                    const uint32_t dw = dsc[u].y;
+                    const int k = static_cast<int>(dw & 0x7fff);
+                    const int s = static_cast<int>(dw >> 16);
+                    const int key = (fl << 16) | k;
+                    if (key != cur) {
                         flush_key();
 #pragma unroll
                         for (int t = 0; t < VEC; ++t) ab[t] = aw[t] = 0.0f;
-                        cur = kk;
-                        if (fl != cur_fl) {
-                            flush_fl();
+                        if constexpr (kRawDb) {
+                            if (fl != db_fl) {
+                                flush_fl();
 #pragma unroll
-                            for (int t = 0; t < VEC; ++t) ad[t] = 0.0f;
-                            cur_fl = fl;
+                                for (int t = 0; t < VEC; ++t) ad[t] = 0.0f;
+                                db_fl = fl;
+                            }
                         }
+                        cur = key;
+                        const int kr = k < B ? k : 0;   // padding: any row (its g is 0)
+                        lds_load_vec<VEC>(s_qw + (static_cast<size_t>(fl) * B + kr) * D + lcx * VEC, wk);
+                        iwk = s_iw[fl * B + kr];
                     }
-                    float dot = 0.0f, dot2 = 0.0f;
+                    float gq[VEC];
+                    float dot = 0.0f;
 #pragma unroll
                     for (int t = 0; t < VEC; ++t) {
-                        const float gr = gv[u][t];
-                        const float gq = quant<Q>(gr);
-                        const float m = valid ? gq : 0.0f;
-                        ab[t] += m;
-                        aw[t] = fmaf(inf.x, m, aw[t]);
-                        ad[t] += valid ? gr : 0.0f;
-                        dot = fmaf(gq, w[t], dot);
-                        dot2 = fmaf(gq, wp[t], dot2);
+                        gq[t] = quant<Q>(gv[u][t]);
+                        ab[t] += gq[t];
+                        aw[t] = fmaf(qf, gq[t], aw[t]);
+                        if constexpr (kRawDb) ad[t] += gv[u][t];
+                        dot = fmaf(gq[t], wk[t], dot);
                     }
                     float part = dot * iwk;
-                    part = edge ? fmaf(dot2, iwp, part) : part;
-                    part = c_ok ? part : 0.0f;
+                    if (dw & 0x8000) {                      // x on the bin's left edge (k >= 1)
+                        float wp[VEC];
+                        lds_load_vec<VEC>(s_qw + (static_cast<size_t>(fl) * B + k - 1) * D + lcx * VEC, wp);
+                        float dot2 = 0.0f;
+#pragma unroll
+                        for (int t = 0; t < VEC; ++t) dot2 = fmaf(gq[t], wp[t], dot2);
+                        part = fmaf(dot2, s_iw[fl * B + k - 1], part);
+                    }
                     if constexpr (LGW_T > 0) part = group_sum<LGW_T>(part);
                     else part = group_sum_rt(part, lgw);
-                    if (lc == 0 && valid) s_dx[p] = part;
+                    if (lc == 0) s_dx[(fl << nt_shift) + s] = part;
                 }
             };
 
+            // Two register buffers: batch b+1 is in flight while batch b is
+            // reduced.  Every issue is unconditional (the one after the last
+            // batch re-reads the slice's first rows and is discarded), so the
+            // loop carries the same loads on every path and the waits stay
+            // per batch.
             const int r0 = lg * R;
             const int r1 = r0 + R;
-            issue(r0, gA);
-            for (int rb = r0; rb < r1; rb += 2 * kUB) {
-                if (rb + kUB < r1) issue(rb + kUB, gB);
-                process(rb, gA);
-                if (rb + 2 * kUB < r1) issue(rb + 2 * kUB, gA);
-                if (rb + kUB < r1) process(rb + kUB, gB);
+            if (R >= 2 * kUB) {
+                issue(r0, gA);
+                for (int rb = r0; rb < r1; rb += 2 * kUB) {
+                    issue(rb + kUB, gB);
+                    process(rb, gA);
+                    issue(rb + 2 * kUB < r1 ? rb + 2 * kUB : r0, gA);
+                    process(rb + kUB, gB);
+                }
+            } else {
+                for (int rb = r0; rb < r1; rb += kUB) {
+                    issue(rb, gA);
+                    process(rb, gA);
+                }
             }
             flush_key();
-            flush_fl();
+            if constexpr (kRawDb) flush_fl();
         }
         __syncthreads();
 
@@ -422,15 +449,14 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
                         sw[t] += rj[D + t];
                     }
                 }
-                const int kfl = key / KB;
-                float *h = s_hist + (static_cast<size_t>(kfl) * B + (key - kfl * KB)) * D2 + lc * VEC;
+                float *h = s_hist + (static_cast<size_t>(key >> 16) * B + (key & 0xffff)) * D2 + lc * VEC;
 #pragma unroll
                 for (int t = 0; t < VEC; ++t) {
                     h[t] += sb[t];
                     h[D + t] += sw[t];
                 }
             }
-            const int rfl = s_rfl[lg];
+            const int rfl = kRawDb ? s_rfl[lg] : -1;
             if (rfl >= 0 && (lg == 0 || s_rfl[lg - 1] != rfl)) {
                 float sd[VEC];
 #pragma unroll
@@ -466,9 +492,11 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
             const int k = (i - fl * B * D2) / D2;
             if (fl < nfh && k < s_nb[fl]) dst[i] = s_hist[i];
         }
-        float *dstb = a.part_db + (static_cast<int64_t>(c) * F + f0) * D;
-        for (int i = tid; i < FS * D; i += kBlock)
-            if (i / D < nfh) dstb[i] = s_db[i];
+        if constexpr (kRawDb) {
+            float *dstb = a.part_db + (static_cast<int64_t>(c) * F + f0) * D;
+            for (int i = tid; i < FS * D; i += kBlock)
+                if (i / D < nfh) dstb[i] = s_db[i];
+        }
     }
 }
 
@@ -605,7 +633,8 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
     const int tid = threadIdx.x;
     const int64_t cstride = static_cast<int64_t>(F) * B * D2;
     const float *src = a.part + static_cast<int64_t>(f) * B * D2;
-    if (a.dw) {
+    const bool need_tot = a.dw || (a.db && a.db_from_buckets);
+    if (need_tot) {
         for (int i = tid; i < n * D2; i += kBlock) {
             float s = 0.0f;
 #pragma unroll 8
@@ -613,6 +642,8 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
             tot[i] = s;
         }
         __syncthreads();
+    }
+    if (a.dw) {
         for (int j = tid; j < D; j += kBlock) {
             float fut = 0.0f;
             for (int k = n - 1; k >= 0; --k) {
@@ -626,7 +657,11 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
     if (a.db) {
         for (int j = tid; j < D; j += kBlock) {
             float s = 0.0f;
-            for (int cc = 0; cc < a.Cd; ++cc) s += a.part_db[(static_cast<int64_t>(cc) * F + f) * D + j];
+            if (a.db_from_buckets) {
+                for (int k = n - 1; k >= 0; --k) s += tot[k * D2 + j];
+            } else {
+                for (int cc = 0; cc < a.Cd; ++cc) s += a.part_db[(static_cast<int64_t>(cc) * F + f) * D + j];
+            }
             a.db[static_cast<int64_t>(f) * D + j] = s;
         }
     }
@@ -670,7 +705,7 @@ size_t fused_layout(BwdArgs &g, int FS, int P, int B, int D, int LG) {
     take(g.o_iw, 4ull * FS * B);
     take(g.o_nb, 4ull * FS);
     take(g.o_info, 8ull * P);
-    take(g.o_order, 2ull * P);
+    take(g.o_order, 8ull * P);
     take(g.o_rank, 1ull * P);
     take(g.o_cnt, 2ull * (P / kWave) * KB);
     take(g.o_seg, 4ull * (FS * KB + 1));
@@ -682,15 +717,17 @@ size_t fused_layout(BwdArgs &g, int FS, int P, int B, int D, int LG) {
     return off;
 }
 
-// g_align: widest vector (elements) the gradient base address allows (1, 2 or 4)
-BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, int g_align) {
+// g_align16: the gradient's base address is 16-byte aligned
+BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16) {
     BwdPlan pl{};
     const int cus = device_cu_count();
     pl.fused = false;
     // fused geometry: VEC=4 rows of D/4 lanes when D allows, else one column
     // per lane; lane groups of a power-of-two width between 2 and 64
-    if (B <= 4096 && env_int("PLE_BWD_SIMPLE", 0) == 0) {
-        const int vec = (D % 4 == 0 && D >= 8 && g_align >= 4) ? 4 : 1;
+    if (B <= 4096 && static_cast<int64_t>(kP) * F * D < INT32_MAX && env_int("PLE_BWD_SIMPLE", 0) == 0) {
+        // 8 floats per lane when D allows (half the lanes, and half the per-row
+        // overhead, of 4 per lane)
+        const int vec = !g_align16 ? 1 : (D % 8 == 0 ? 8 : (D % 4 == 0 && D >= 8 ? 4 : 1));
         const int uv = static_cast<int>(D / vec);
         int lgw = 2;
         while (lgw < uv) lgw *= 2;
@@ -780,9 +817,15 @@ hipError_t launch_fused_idx(const BwdArgs &a, int idxb, dim3 grid, size_t lds, h
 // reductions); the one-column-per-lane variant takes it at run time.
 template <int GD, int Q>
 hipError_t launch_fused(const BwdArgs &a, int vec, int idxb, dim3 grid, size_t lds, hipStream_t s) {
+    if (vec == 8) {
+        switch (a.LGW) {
+            case 2: return launch_fused_idx<GD, Q, 8, 2>(a, idxb, grid, lds, s);
+            case 4: return launch_fused_idx<GD, Q, 8, 4>(a, idxb, grid, lds, s);
+            default: return launch_fused_idx<GD, Q, 8, 8>(a, idxb, grid, lds, s);
+        }
+    }
     if (vec == 4) {
         switch (a.LGW) {
-            case 2: return launch_fused_idx<GD, Q, 4, 2>(a, idxb, grid, lds, s);
             case 4: return launch_fused_idx<GD, Q, 4, 4>(a, idxb, grid, lds, s);
             case 8: return launch_fused_idx<GD, Q, 4, 8>(a, idxb, grid, lds, s);
             default: return launch_fused_idx<GD, Q, 4, 16>(a, idxb, grid, lds, s);
@@ -795,6 +838,7 @@ template <int GD, int Q>
 hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bool want_dwdb, hipStream_t s) {
     hipError_t e = hipSuccess;
     if (pl.fused) {
+        a.db_from_buckets = Q == PLE_DTYPE_F32;
         const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.G) * pl.C));
         e = launch_fused<GD, Q>(a, pl.vec, idxb, grid, pl.lds, s);
         if (e != hipSuccess) return e;
@@ -846,12 +890,9 @@ hipError_t launch_q(const BwdArgs &a, const BwdPlan &pl, int q, int idxb, bool w
 
 size_t backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D) {
     // the plan depends on the gradient's alignment; report the largest need
-    size_t m = 0;
-    for (int al = 1; al <= 4; al *= 2) {
-        const size_t t = plan_backward(N, F, B, D, al).total();
-        m = t > m ? t : m;
-    }
-    return m;
+    const size_t a = plan_backward(N, F, B, D, true).total();
+    const size_t b = plan_backward(N, F, B, D, false).total();
+    return a > b ? a : b;
 }
 
 int backward_run(const BackwardRequest &r) {
@@ -861,8 +902,7 @@ int backward_run(const BackwardRequest &r) {
     const uintptr_t gaddr = reinterpret_cast<uintptr_t>(r.g);
     const int gbytes = r.grad_dtype == PLE_DTYPE_F32 ? 4 : 2;
     if (gaddr % gbytes != 0) return PLE_E_MISALIGNED;
-    const int g_align = gaddr % (4 * gbytes) == 0 ? 4 : (gaddr % (2 * gbytes) == 0 ? 2 : 1);
-    BwdPlan pl = plan_backward(r.N, r.F, r.B, r.D, g_align);
+    BwdPlan pl = plan_backward(r.N, r.F, r.B, r.D, gaddr % 16 == 0);
     if (!pl.fused && want_dwdb && pl.lds > kLdsMax) return PLE_E_UNSUPPORTED;
     const size_t need = pl.total();
     if (want_dwdb && (r.workspace == nullptr || r.workspace_bytes < need ||

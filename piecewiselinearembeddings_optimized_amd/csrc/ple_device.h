@@ -63,12 +63,18 @@ __device__ __forceinline__ float load_grad(const void *p, int64_t i) {
 }
 
 // Loads VEC consecutive gradient elements starting at element i (i is a
-// multiple of VEC; the base is aligned for the vector width).
+// multiple of VEC; the base is aligned for the vector width).  VEC in
+// {1, 2, 4, 8}.
 template <int G, int VEC>
 __device__ __forceinline__ void load_grad_vec(const void *p, int64_t i, float *out) {
     if constexpr (G == PLE_DTYPE_F32) {
         const float *q = static_cast<const float *>(p) + i;
-        if constexpr (VEC == 4) {
+        if constexpr (VEC == 8) {
+            const float4 v0 = reinterpret_cast<const float4 *>(q)[0];
+            const float4 v1 = reinterpret_cast<const float4 *>(q)[1];
+            out[0] = v0.x; out[1] = v0.y; out[2] = v0.z; out[3] = v0.w;
+            out[4] = v1.x; out[5] = v1.y; out[6] = v1.z; out[7] = v1.w;
+        } else if constexpr (VEC == 4) {
             const float4 v = *reinterpret_cast<const float4 *>(q);
             out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
         } else if constexpr (VEC == 2) {
@@ -80,7 +86,11 @@ __device__ __forceinline__ void load_grad_vec(const void *p, int64_t i, float *o
     } else {
         const uint16_t *q = static_cast<const uint16_t *>(p) + i;
         uint16_t h[VEC];
-        if constexpr (VEC == 4) {
+        if constexpr (VEC == 8) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(q);
+            h[0] = v.x & 0xffffu; h[1] = v.x >> 16; h[2] = v.y & 0xffffu; h[3] = v.y >> 16;
+            h[4] = v.z & 0xffffu; h[5] = v.z >> 16; h[6] = v.w & 0xffffu; h[7] = v.w >> 16;
+        } else if constexpr (VEC == 4) {
             const uint2 v = *reinterpret_cast<const uint2 *>(q);
             h[0] = v.x & 0xffffu; h[1] = v.x >> 16; h[2] = v.y & 0xffffu; h[3] = v.y >> 16;
         } else if constexpr (VEC == 2) {
@@ -92,6 +102,34 @@ __device__ __forceinline__ void load_grad_vec(const void *p, int64_t i, float *o
 #pragma unroll
         for (int t = 0; t < VEC; ++t)
             out[t] = (G == PLE_DTYPE_BF16) ? bf16_to_float(h[t]) : f16_to_float(h[t]);
+    }
+}
+
+// VEC consecutive floats from / to LDS (16-byte accesses for VEC 4 and 8;
+// the address is 16-byte aligned in those cases).
+template <int VEC>
+__device__ __forceinline__ void lds_load_vec(const float *p, float *v) {
+    if constexpr (VEC % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < VEC / 4; ++q) {
+            const float4 t = reinterpret_cast<const float4 *>(p)[q];
+            v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < VEC; ++t) v[t] = p[t];
+    }
+}
+
+template <int VEC>
+__device__ __forceinline__ void lds_store_vec(float *p, const float *v) {
+    if constexpr (VEC % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < VEC / 4; ++q)
+            reinterpret_cast<float4 *>(p)[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    } else {
+#pragma unroll
+        for (int t = 0; t < VEC; ++t) p[t] = v[t];
     }
 }
 

@@ -45,6 +45,8 @@ size_t fwd_lds_bytes(int FS, int B, int D) {
                 + static_cast<size_t>(FS));           // n_bins
 }
 
+constexpr int kStoreUnroll = 4;
+
 template <int Q, int OUT, bool HAS_BIAS, int VEC, typename IdxT>
 __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
     extern __shared__ float smem[];
@@ -167,35 +169,54 @@ __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
     const int64_t n_tiles = (rows + SW - 1) / SW;
     const int64_t row_elems = static_cast<int64_t>(F) * D;
 
+    // x of the wave's next tile is loaded while the current tile is stored
+    // (an out-of-range lane reads x[0] and ignores it, so the load has no
+    // branch around it)
+    auto load_x = [&](int64_t t) __attribute__((always_inline)) -> float {
+        const int64_t pn = n_begin + t * SW + p_s;
+        const bool ok = p_fok && (t < n_tiles) && (pn < n_end);
+        return a.x[ok ? pn * F + f0 + p_fl : 0];
+    };
+    float v_next = load_x(wave);
+
     for (int64_t t = wave; t < n_tiles; t += kWavesPerBlock) {
         const int64_t n0 = n_begin + t * SW;
         const int64_t pn = n0 + p_s;
         const bool pvalid = p_fok && (pn < n_end);
         const int64_t pidx = pn * F + f0 + p_fl;
-        const float v = pvalid ? a.x[pidx] : 0.0f;
+        const float v = pvalid ? v_next : 0.0f;
+        v_next = load_x(t + kWavesPerBlock);
         const int k = find_bin(v, e_row, p_n);
         const float frac = (v - e_row[k]) * iw_row[k];
         const float qf = quant<Q>(frac);
         if (pvalid) static_cast<IdxT *>(a.idx)[pidx] = static_cast<IdxT>(k);
 
-        for (int sb = 0; sb < SW; sb += R) {
-            const int s = sb + o_s;
-            const int src = (s * FS + o_fl) & (kWave - 1);
-            const int ks = __shfl(k, src);
-            const float qs = __shfl(qf, src);
-            const int64_t n = n0 + s;
-            if (o_ok && s < SW && n < n_end) {
-                const float *row = o_tbl + static_cast<size_t>(ks) * rs;
+        // kStoreUnroll store instructions per step: their shuffles and table
+        // reads are issued together, then the stores
+        for (int sb = 0; sb < SW; sb += R * kStoreUnroll) {
+            int ks[kStoreUnroll];
+            float qs[kStoreUnroll];
+#pragma unroll
+            for (int q = 0; q < kStoreUnroll; ++q) {
+                const int src = ((sb + q * R + o_s) * FS + o_fl) & (kWave - 1);
+                ks[q] = __shfl(k, src);
+                qs[q] = __shfl(qf, src);
+            }
+#pragma unroll
+            for (int q = 0; q < kStoreUnroll; ++q) {
+                const int s = sb + q * R + o_s;
+                const int64_t n = n0 + s;
+                const float *row = o_tbl + static_cast<size_t>(ks[q]) * rs;
                 float r[VEC];
                 if constexpr (VEC == 4) {
                     const float4 P = *reinterpret_cast<const float4 *>(row);
                     const float4 W = *reinterpret_cast<const float4 *>(row + D);
-                    r[0] = fmaf(qs, W.x, P.x);
-                    r[1] = fmaf(qs, W.y, P.y);
-                    r[2] = fmaf(qs, W.z, P.z);
-                    r[3] = fmaf(qs, W.w, P.w);
+                    r[0] = fmaf(qs[q], W.x, P.x);
+                    r[1] = fmaf(qs[q], W.y, P.y);
+                    r[2] = fmaf(qs[q], W.z, P.z);
+                    r[3] = fmaf(qs[q], W.w, P.w);
                 } else {
-                    r[0] = fmaf(qs, row[D], row[0]);
+                    r[0] = fmaf(qs[q], row[D], row[0]);
                 }
 #pragma unroll
                 for (int t2 = 0; t2 < VEC; ++t2) {
@@ -203,13 +224,17 @@ __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
                     if constexpr (HAS_BIAS) o = o + bvec[t2];
                     r[t2] = o;
                 }
-                store_out<OUT, VEC>(a.out, n * row_elems + static_cast<int64_t>(f0 + o_fl) * D + o_u * VEC, r);
+                if (o_ok && s < SW && n < n_end)
+                    store_out<OUT, VEC>(a.out, n * row_elems + static_cast<int64_t>(f0 + o_fl) * D + o_u * VEC, r);
             }
         }
     }
 }
 
-constexpr size_t kLdsBudgetTwoPerCu = 80 * 1024;
+// LDS per workgroup the planner aims for: small tables keep many workgroups
+// (and their loads) in flight per CU, which the store stream needs more than
+// wide feature groups.
+constexpr size_t kLdsBudget = 24 * 1024;
 
 int env_int(const char *name, int dflt) {
     const char *s = getenv(name);
@@ -224,16 +249,16 @@ struct FwdPlan {
 };
 
 // FS: the widest power-of-two feature group whose row fits one wave's stores
-// (FS * D/VEC <= 64) and whose tables fit the LDS budget for two workgroups
-// per CU.  Chunks: about 8 workgroups per CU over the grid, a multiple of the
-// XCD count.  PLE_FWD_FS / PLE_FWD_WG_PER_CU override the two choices (tuning).
+// (FS * D/VEC <= 64) and whose tables fit kLdsBudget.  Chunks: about 32
+// workgroups per CU over the grid, a multiple of the XCD count.
+// PLE_FWD_FS / PLE_FWD_WG_PER_CU override the two choices (tuning).
 bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, bool aligned16, FwdPlan &pl) {
     pl.vec = (D % 4 == 0 && aligned16) ? 4 : 1;
     const int U = static_cast<int>(D / pl.vec);
     if (U > kWave) return false;
     int fs = 1;
     while (fs * 2 <= kWave && fs * 2 * U <= kWave && fs < F) fs *= 2;
-    while (fs > 1 && fwd_lds_bytes(fs, static_cast<int>(B), static_cast<int>(D)) > kLdsBudgetTwoPerCu) fs /= 2;
+    while (fs > 1 && fwd_lds_bytes(fs, static_cast<int>(B), static_cast<int>(D)) > kLdsBudget) fs /= 2;
     const int fs_env = env_int("PLE_FWD_FS", 0);
     if (fs_env > 0 && (fs_env & (fs_env - 1)) == 0 && fs_env * U <= kWave &&
         fwd_lds_bytes(fs_env, static_cast<int>(B), static_cast<int>(D)) <= kLdsMax)
@@ -242,7 +267,7 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, bool aligned16, Fw
     if (pl.lds > kLdsMax) return false;
     pl.FS = fs;
     pl.G = static_cast<int>((F + fs - 1) / fs);
-    const int target = env_int("PLE_FWD_WG_PER_CU", 8) * device_cu_count();
+    const int target = env_int("PLE_FWD_WG_PER_CU", 32) * device_cu_count();
     int64_t c = (target + pl.G - 1) / pl.G;
     const int64_t sw = kWave / fs;
     const int64_t max_c = (N + sw - 1) / sw;          // at least one wave tile per chunk
