@@ -74,7 +74,10 @@ int ple_bin_index_bytes(int64_t max_n_bins);
  *                   int16 / int32)
  *   quant_dtype     PLE_DTYPE_* used for q() and round_quant()
  *   output_dtype    PLE_DTYPE_* of the stored output
- * N may be 0 (no launch).  F, B, D >= 1.
+ * Supported pairings: output_dtype == quant_dtype with bias NULL (the
+ * reference operator), or output_dtype == PLE_DTYPE_F32 with a bias (the
+ * module's "x_ple + bias" fused into the store); others -> PLE_E_UNSUPPORTED.
+ * N may be 0 (no launch).  F, B, D >= 1; D <= 64; B <= 32766.
  */
 int ple_forward_launch(const float *x, const float *bin_edges, const float *inv_bin_widths,
                        const int32_t *n_bins, const float *weight, const float *bias,
@@ -90,8 +93,11 @@ size_t ple_backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D);
  *                   + [k > 0 and x == e_k] * iw_{k-1} * <g, q(W[f, k-1])>
  *   grad_weight[f, phys(k)] = sum_{bin=k} q(frac) g + sum_{bin>k} g
  *                   (slots no bin maps to are written as 0)
- *   grad_bias[f]  = sum_n grad_output[n, f]
+ *   grad_bias[f]  = sum_n grad_output[n, f]   (unrounded grad_output)
  * where g = grad_output rounded through quant_dtype (identity for F32).
+ * Supported pairings: quant_dtype == grad_dtype (the reference operator,
+ * whose gradient arrives in the forward's output dtype), or grad_dtype ==
+ * PLE_DTYPE_F32 with any quant_dtype; others -> PLE_E_UNSUPPORTED.
  * Each of grad_x / grad_weight / grad_bias may be NULL (not computed).
  * Reductions are deterministic: a fixed summation order, no atomics on
  * floating-point data.

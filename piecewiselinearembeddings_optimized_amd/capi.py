@@ -1,0 +1,101 @@
+"""ctypes binding of the C ABI in ``include/ple_hip.h`` (``libple_hip.so``).
+
+This is the binding a caller without the torch operators would use: plain
+device pointers, sizes, dtype codes and a stream handle.  The helpers below
+take torch tensors only to read their pointers and sizes; nothing here copies
+or allocates except :func:`backward`, which takes a workspace from the caller
+or allocates one through torch.
+
+Every entry point returns an ``int`` code; non-zero codes raise
+:class:`PleError` with ``ple_error_string``'s text.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libple_hip.so")
+
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+_DTYPE_CODES = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
+
+_lib = None
+
+
+class PleError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{message} (code {code})")
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    """Loads ``libple_hip.so`` once and declares every prototype."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"{_LIB_PATH} is not built; run piecewiselinearembeddings_optimized_amd._build")
+        L = ctypes.CDLL(_LIB_PATH)
+        p, i64, i32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
+        L.ple_abi_version.argtypes, L.ple_abi_version.restype = [], i32
+        L.ple_bin_index_bytes.argtypes, L.ple_bin_index_bytes.restype = [i64], i32
+        L.ple_error_string.argtypes, L.ple_error_string.restype = [i32], ctypes.c_char_p
+        L.ple_forward_launch.argtypes = [p, p, p, p, p, p, p, p, i64, i64, i64, i64, i32, i32, p]
+        L.ple_forward_launch.restype = i32
+        L.ple_backward_workspace_bytes.argtypes = [i64, i64, i64, i64]
+        L.ple_backward_workspace_bytes.restype = sz
+        L.ple_backward_launch.argtypes = [p, p, p, p, p, p, p, p, p, p, i64, i64, i64, i64, i32, i32, p, sz, p]
+        L.ple_backward_launch.restype = i32
+        _lib = L
+    return _lib
+
+
+def check(code: int) -> None:
+    if code != 0:
+        raise PleError(code, lib().ple_error_string(code).decode())
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    return _DTYPE_CODES[dtype]
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def forward(x, bin_edges, inv_bin_widths, n_bins, weight, bias, output, bin_indices, quant_dtype,
+            stream=None) -> None:
+    """``ple_forward_launch`` into caller-provided ``output`` / ``bin_indices``."""
+    n, f = x.shape
+    _, bmax, d = weight.shape
+    check(lib().ple_forward_launch(
+        _ptr(x), _ptr(bin_edges), _ptr(inv_bin_widths), _ptr(n_bins), _ptr(weight), _ptr(bias),
+        _ptr(output), _ptr(bin_indices), n, f, bmax, d, dtype_code(quant_dtype), dtype_code(output.dtype),
+        _stream(stream)))
+
+
+def workspace_bytes(n: int, f: int, bmax: int, d: int) -> int:
+    return int(lib().ple_backward_workspace_bytes(n, f, bmax, d))
+
+
+def backward(grad_output, x, bin_edges, inv_bin_widths, n_bins, weight, bin_indices, grad_x, grad_weight,
+             grad_bias, quant_dtype, workspace=None, stream=None) -> None:
+    """``ple_backward_launch``; ``grad_*`` are caller-provided fp32 tensors or None."""
+    n, f = x.shape
+    _, bmax, d = weight.shape
+    need = workspace_bytes(n, f, bmax, d)
+    if workspace is None and need > 0:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib().ple_backward_launch(
+        _ptr(grad_output), _ptr(x), _ptr(bin_edges), _ptr(inv_bin_widths), _ptr(n_bins), _ptr(weight),
+        _ptr(bin_indices), _ptr(grad_x), _ptr(grad_weight), _ptr(grad_bias), n, f, bmax, d,
+        dtype_code(grad_output.dtype), dtype_code(quant_dtype), _ptr(workspace), ws_bytes, _stream(stream)))

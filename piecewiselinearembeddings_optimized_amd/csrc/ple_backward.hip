@@ -6,30 +6,40 @@
 //                                                 reference backward_cuda.cu:170-336,889-923
 // db[f]    = sum_n g                              (autograd of module.py:238-239)
 //
-// Main path, ple_bwd_fused_kernel: one pass over grad_output.  A workgroup
-// owns FS features and a chunk of samples, and walks the chunk in sub-tiles
-// of P (sample, feature) pairs.  Per sub-tile it
-//   A. reads the bin index and x of every pair (coalesced along the group's
-//      features), computes q(frac) and the edge flag;
-//   B-D. counting-sorts the pairs by (feature, bin): per 64-pair block, ranks
-//      of equal keys from 64-bit ballots, a per-key prefix over blocks and a
-//      block-wide scan over keys -- deterministic and stable;
-//   F. lets lane groups (D/VEC lanes, one row of grad_output per step) walk
-//      equal slices of the sorted rows: each row is read once, its dx is the
-//      lane group's shuffle-reduced dot with the LDS weight row, and bucket /
-//      weighted / bias sums run in registers until the key changes.  A slice's
-//      first key goes to a per-slice record, every later key is added straight
-//      into the LDS histogram (no other slice can own it);
-//   G. adds the records, run by run in slice order, into the histogram;
-//   H. stores dx.
-// The chunk's histogram is written once; ple_bwd_finalize_kernel sums the
-// chunks in chunk order and takes the suffix over bins.  No floating-point
-// atomics anywhere, a fixed order for every sum, so results repeat bitwise.
+// Main path: two kernels over tiles of P (sample, feature) pairs (NT samples
+// x FS features, "sub-tiles").
+//
+// ple_bwd_sort_kernel -- one workgroup per sub-tile.  Reads the bin index and
+//   x of every pair, computes q(frac) and the edge flag, and counting-sorts
+//   the pairs by (feature, bin): per 64-pair block, ranks of equal keys from
+//   64-bit ballots, a per-key prefix over blocks and a block-wide scan over
+//   keys -- deterministic and stable.  Writes the sorted row descriptors
+//   {q(frac) (-0 marks x on the bin's left edge), sample | feature << 24} and
+//   the sub-tile's pieces: every (feature, bin) run of sorted rows cut into
+//   pieces of kL rows.
+//
+// ple_bwd_reduce_kernel -- one workgroup per feature group and chunk of
+//   sub-tiles; nothing but the gradient stream and LDS work.  Lane groups
+//   (D/VEC lanes, one grad_output row per step) take equal runs of pieces:
+//   each row is read once, its dx is the lane group's DPP-reduced dot with
+//   the LDS weight row (written straight to dx), and bucket / weighted / bias
+//   sums run in registers until the key changes (checked once per piece).
+//   A run's first key goes to a per-run record, every later key straight into
+//   the LDS histogram (no other run can own it); the records are added run
+//   by run in order.  The next sub-tile's descriptors travel while the
+//   current one is reduced.  The chunk's histogram is written once;
+//   ple_bwd_finalize_kernel sums the chunks in chunk order and takes the
+//   suffix over bins.
+//
+// No floating-point atomics anywhere, a fixed order for every sum, so results
+// repeat bitwise.
 //
 // Fallback (shapes whose tables do not fit LDS): ple_bwd_simple_dx_kernel and
 // ple_bwd_simple_hist_kernel, same partial layout, same finalize.
 
 #include <stdlib.h>
+
+#include <algorithm>
 
 #include "ple_device.h"
 #include "ple_internal.h"
@@ -48,24 +58,24 @@ struct BwdArgs {
     float *dx;
     float *dw;
     float *db;
-    float *part;     // [C][F][B][2D] chunk partials {bucket | weighted}
-    float *part_db;  // [C][F][D] chunk partials of the bias gradient
+    float *part;     // [Cd][F][B][2D] chunk partials {bucket | weighted}
+    float *part_db;  // [Cd][F][D] chunk partials of the bias gradient
+    uint2 *desc;     // [T][G][P] sorted row descriptors {q(frac) (-0: edge row), sample | fl << 24}
+    uint32_t *piece; // [T][G][PM] pieces {bin | fl << 12 | first row << 16 | (rows - 1) << 28}
+    int *npc;        // [T][G] pieces per sub-tile
+    float *dxt;      // [F][N] dx, feature-major (transposed into dx at the end)
     int64_t N;
     int F, B, D;
-    int C;           // chunks in the grid (fused: a multiple of kNumXcd)
+    int C;           // chunks (fallback: of samples; sorted path: of sub-tiles)
     int Cd;          // chunks holding samples (the ones that write partials)
-    int64_t NC;      // samples per chunk
+    int64_t NC;      // fallback: samples per chunk
     int db_from_buckets;   // finalize: db = sum of the bin buckets (no raw-gradient partials)
-    // fused path
-    int FS, G, NT, P, LGW, nbits;   // P: pairs per sub-tile (kP)
-    int o_qw, o_hist, o_db, o_edge, o_iw, o_nb, o_info, o_order, o_rank, o_cnt, o_seg, o_dx, o_rec,
-        o_rkey, o_rfl, o_tmp;
+    int fin_direct;        // finalize: chunk sums read straight from the partials (no LDS table)
+    // sorted path
+    int FS, G, NT, T, SPC, PM, LGW, nbits;   // T sub-tiles, SPC sub-tiles per chunk, PM piece capacity
+    int so_nb, so_edge, so_iw, so_info, so_rank, so_cnt, so_seg, so_tmp, so_desc, so_piece;   // sort LDS
+    int ro_qw, ro_hist, ro_db, ro_iw, ro_nb, ro_desc, ro_piece, ro_npc, ro_rec, ro_rkey, ro_rfl, ro_dx, ro_inv;   // reduce LDS
 };
-
-// A row of zeros in device memory: padding rows and idle lanes of the fused
-// kernel load from here, so their contributions are exact zeros without any
-// masking in the row loop.  Never written.
-__device__ __attribute__((aligned(16))) float g_zero_row[64] = {};
 
 // Exclusive prefix sum of a[0..n) in place, all kBlock threads.
 __device__ void block_exclusive_scan(int *a, int n, int *tmp) {
@@ -97,72 +107,234 @@ __device__ void block_exclusive_scan(int *a, int n, int *tmp) {
 
 constexpr int kP = 1024;                        // (sample, feature) pairs per sub-tile
 constexpr int kPairsPerThread = kP / kBlock;
-constexpr int kRowRegs = 32;                    // gradient floats per lane in one prefetch batch (phase F)
+constexpr int kMaxBlocksPerFeature = kP / kWave;
+// Rows per piece: every (feature, bin) run of a sorted sub-tile is cut into
+// pieces of kL consecutive rows (the last one shorter).
+constexpr int kL = 4;
+// Piece capacity per sub-tile: at most P / kL + (non-empty keys) pieces.
+constexpr int kMaxPieces = kP / kL + kP;
+constexpr int kPieceRegs = (kMaxPieces + kBlock - 1) / kBlock;
 
-template <int GD, int Q, int VEC, int LGW_T, typename IdxT>
-__global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
-    constexpr int kUB = VEC == 8 ? kRowRegs / 8 : 8;   // sorted rows per prefetch batch
+// ---------------------------------------------------------------------------
+// sort
+// ---------------------------------------------------------------------------
+
+template <int Q, typename IdxT>
+__global__ __launch_bounds__(kBlock) void ple_bwd_sort_kernel(BwdArgs a) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int FS = a.FS, B = a.B, F = a.F, NT = a.NT;
+    const int KB = B + 1;                   // keys per feature; key B marks padding rows
+    int *s_nb = reinterpret_cast<int *>(lds + a.so_nb);                 // [FS]
+    float *s_edge = reinterpret_cast<float *>(lds + a.so_edge);         // [FS][B+1]
+    float *s_iw = reinterpret_cast<float *>(lds + a.so_iw);             // [FS][B]
+    float2 *s_info = reinterpret_cast<float2 *>(lds + a.so_info);       // [P] {q(frac), key|edge}
+    uint8_t *s_rank = reinterpret_cast<uint8_t *>(lds + a.so_rank);     // [P]
+    uint16_t *s_cnt = reinterpret_cast<uint16_t *>(lds + a.so_cnt);     // [P/64][B+1]
+    int *s_seg = reinterpret_cast<int *>(lds + a.so_seg);               // [FS*(B+1)] {start | first piece << 16}
+    int *s_tmp = reinterpret_cast<int *>(lds + a.so_tmp);               // [kWavesPerBlock]
+    uint2 *s_sdesc = reinterpret_cast<uint2 *>(lds + a.so_desc);        // [P]
+    uint32_t *s_piece = reinterpret_cast<uint32_t *>(lds + a.so_piece); // [PM]
+
+    int g, t;
+    if (!decode_tile(blockIdx.x, a.G, a.T, g, t)) return;
+    const int f0 = g * FS;
+    const int nfh = min(FS, F - f0);
+    const int64_t sub = static_cast<int64_t>(t) * NT;
+    const int ns = static_cast<int>(min(static_cast<int64_t>(NT), a.N - sub));
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    const int NB = kP / kWave;                    // 64-pair blocks per sub-tile
+    const int NBf = NT / kWave;                   // blocks per feature
+
+    // pair inputs: thread -> pairs i = tid + u * kBlock, i -> (sample i / FS,
+    // feature i % FS); unconditional loads (pair 0 stands in for padding)
+    int pk[kPairsPerThread];
+    float pv[kPairsPerThread];
+#pragma unroll
+    for (int u = 0; u < kPairsPerThread; ++u) {
+        const int i = tid + u * kBlock;
+        const int s = i / FS;
+        const int fl = i - s * FS;
+        const int64_t pair = (s < ns && fl < nfh) ? (sub + s) * F + f0 + fl : 0;
+        pk[u] = load_idx<IdxT>(a.idx, pair);
+        pv[u] = a.x[pair];
+    }
+    for (int i = tid; i < FS; i += kBlock) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
+    for (int i = tid; i < FS * KB; i += kBlock) {
+        const int fl = i / KB;
+        s_edge[i] = fl < nfh ? a.edges[static_cast<int64_t>(f0) * KB + i] : 0.0f;
+    }
+    for (int i = tid; i < FS * B; i += kBlock) {
+        const int fl = i / B;
+        s_iw[i] = fl < nfh ? a.iw[static_cast<int64_t>(f0) * B + i] : 0.0f;
+    }
+    for (int i = tid; i < NB * KB; i += kBlock) s_cnt[i] = 0;
+    __syncthreads();
+
+    // A. pair info, stored feature-major (p = fl * NT + s)
+#pragma unroll
+    for (int u = 0; u < kPairsPerThread; ++u) {
+        const int i = tid + u * kBlock;
+        const int s = i / FS;
+        const int fl = i - s * FS;
+        int key = B;
+        float qf = 0.0f;
+        if (s < ns && fl < nfh) {
+            const int k = clamp_bin(pk[u], s_nb[fl]);
+            const float v = pv[u];
+            const float e = s_edge[fl * KB + k];
+            qf = quant<Q>((v - e) * s_iw[fl * B + k]);
+            key = k | ((k > 0 && v == e) ? 0x8000 : 0);
+        }
+        s_info[fl * NT + s] = make_float2(qf, __int_as_float(key));
+    }
+    __syncthreads();
+
+    // B. rank of each pair among equal keys of its 64-pair block
+    for (int b = wave; b < NB; b += kWavesPerBlock) {
+        const int p = b * kWave + lane;
+        const int k = __float_as_int(s_info[p].y) & 0x7fff;
+        unsigned long long m = ~0ull;
+        for (int bit = 0; bit < a.nbits; ++bit) {
+            const bool set = (k >> bit) & 1;
+            const unsigned long long bal = __ballot(set);
+            m &= set ? bal : ~bal;
+        }
+        const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+        const int rank = __popcll(m & lt);
+        s_rank[p] = static_cast<uint8_t>(rank);
+        if (rank == 0) s_cnt[b * KB + k] = static_cast<uint16_t>(__popcll(m));
+    }
+    __syncthreads();
+
+    // C. per key: exclusive prefix of its counts over the feature's blocks
+    //    (held in registers), then {count | pieces << 16} for the scan
+    for (int kk = tid; kk < FS * KB; kk += kBlock) {
+        const int fl = kk / KB;
+        const int k = kk - fl * KB;
+        uint16_t *col = s_cnt + fl * NBf * KB + k;
+        int cc[kMaxBlocksPerFeature];
+#pragma unroll
+        for (int bb = 0; bb < kMaxBlocksPerFeature; ++bb) cc[bb] = bb < NBf ? col[bb * KB] : 0;
+        int run = 0;
+#pragma unroll
+        for (int bb = 0; bb < kMaxBlocksPerFeature; ++bb) {
+            if (bb < NBf) col[bb * KB] = static_cast<uint16_t>(run);
+            run += cc[bb];
+        }
+        const int pieces = k < B ? (run + kL - 1) / kL : 0;   // padding rows (key B): none
+        s_seg[kk] = run | (pieces << 16);
+    }
+    __syncthreads();
+    // run starts (low half) and first piece of each run (high half); neither
+    // sum reaches 2^16
+    block_exclusive_scan(s_seg, FS * KB, s_tmp);
+
+    // D. scatter: sorted position -> row descriptor; the first row of every
+    //    piece writes the piece's entry
+    for (int p = tid; p < kP; p += kBlock) {
+        const int fl = p / NT;
+        const int s = p - fl * NT;
+        const float2 inf = s_info[p];
+        const int kb = __float_as_int(inf.y);
+        const int k = kb & 0x7fff;
+        const int sg = s_seg[fl * KB + k];
+        const int within = s_cnt[(p / kWave) * KB + k] + s_rank[p];
+        const int slot = (sg & 0xffff) + within;
+        // x on e_k (k >= 1) gives q(frac) == +0 exactly; such rows carry -0
+        // instead, which marks the edge term and adds the same zero.  A -0
+        // from anywhere else becomes +0 (the same contribution).
+        uint32_t qbits = __float_as_uint(inf.x);
+        qbits = (kb & 0x8000) ? 0x80000000u : (qbits == 0x80000000u ? 0u : qbits);
+        s_sdesc[slot] = make_uint2(qbits, static_cast<uint32_t>(s) | (static_cast<uint32_t>(fl) << 24));
+        if (k < B && within % kL == 0) {
+            // the run ends where the next key's (at least the padding key B) begins
+            const int end = s_seg[fl * KB + k + 1] & 0xffff;
+            const int rows = min(kL, end - slot);
+            s_piece[(sg >> 16) + within / kL] = static_cast<uint32_t>(k) | (static_cast<uint32_t>(fl) << 12) |
+                                                (static_cast<uint32_t>(slot) << 16) |
+                                                (static_cast<uint32_t>(rows - 1) << 28);
+        }
+    }
+    __syncthreads();
+
+    // out: descriptors (16-byte stores), pieces, piece count
+    const int64_t tile = static_cast<int64_t>(t) * a.G + g;
+    uint4 *ddst = reinterpret_cast<uint4 *>(a.desc + tile * kP);
+    const uint4 *dsrc = reinterpret_cast<const uint4 *>(s_sdesc);
+    for (int i = tid; i < kP / 2; i += kBlock) ddst[i] = dsrc[i];
+    const int npc = s_seg[FS * KB - 1] >> 16;     // the last key is padding: no pieces of its own
+    uint32_t *pdst = a.piece + tile * a.PM;
+    for (int i = tid; i < npc; i += kBlock) pdst[i] = s_piece[i];
+    if (tid == 0) a.npc[tile] = npc;
+}
+
+// ---------------------------------------------------------------------------
+// reduce
+// ---------------------------------------------------------------------------
+
+template <int GD, int Q, int VEC, int LGW_T>
+__global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
     // With fp32 rounding the bias gradient is the sum of the bin buckets
     // (taken at finalize); otherwise it needs its own sum of the unrounded
     // gradient.
     constexpr bool kRawDb = Q != PLE_DTYPE_F32;
     extern __shared__ __align__(16) unsigned char lds[];
     const int FS = a.FS, B = a.B, D = a.D, F = a.F, NT = a.NT;
-    const int KB = B + 1;                   // keys per feature; key B marks padding rows
-    float *s_qw = reinterpret_cast<float *>(lds + a.o_qw);        // [FS][B][D]
-    float *s_hist = reinterpret_cast<float *>(lds + a.o_hist);    // [FS][B][2D]
-    float *s_db = reinterpret_cast<float *>(lds + a.o_db);        // [FS][D]
-    float *s_edge = reinterpret_cast<float *>(lds + a.o_edge);    // [FS][B+1]
-    float *s_iw = reinterpret_cast<float *>(lds + a.o_iw);        // [FS][B]
-    int *s_nb = reinterpret_cast<int *>(lds + a.o_nb);            // [FS]
-    float2 *s_info = reinterpret_cast<float2 *>(lds + a.o_info);  // [P] {q(frac), key|edge}
-    uint2 *s_sdesc = reinterpret_cast<uint2 *>(lds + a.o_order);        // [P] sorted rows {q(frac), key|edge|s<<16}
-    uint8_t *s_rank = reinterpret_cast<uint8_t *>(lds + a.o_rank);      // [P]
-    uint16_t *s_cnt = reinterpret_cast<uint16_t *>(lds + a.o_cnt);      // [P/64][B+1]
-    int *s_seg = reinterpret_cast<int *>(lds + a.o_seg);                // [FS*(B+1)]
-    float *s_dx = reinterpret_cast<float *>(lds + a.o_dx);              // [P]
-    float *s_rec = reinterpret_cast<float *>(lds + a.o_rec);            // [LG][3D]
-    int *s_rkey = reinterpret_cast<int *>(lds + a.o_rkey);              // [LG]
-    int *s_rfl = reinterpret_cast<int *>(lds + a.o_rfl);                // [LG]
-    int *s_tmp = reinterpret_cast<int *>(lds + a.o_tmp);                // [kWavesPerBlock]
+    float *s_qw = reinterpret_cast<float *>(lds + a.ro_qw);             // [FS][B][D]
+    float *s_hist = reinterpret_cast<float *>(lds + a.ro_hist);         // [FS][B][2D]
+    float *s_db = reinterpret_cast<float *>(lds + a.ro_db);             // [FS][D]
+    float *s_iw = reinterpret_cast<float *>(lds + a.ro_iw);             // [FS][B]
+    int *s_nb = reinterpret_cast<int *>(lds + a.ro_nb);                 // [FS]
+    uint2 *s_sdesc = reinterpret_cast<uint2 *>(lds + a.ro_desc);        // [P+1]: sorted rows, then a dummy row
+    uint32_t *s_piece = reinterpret_cast<uint32_t *>(lds + a.ro_piece); // [PM]
+    int *s_npc = reinterpret_cast<int *>(lds + a.ro_npc);               // [1]
+    float *s_rec = reinterpret_cast<float *>(lds + a.ro_rec);           // [LG][RS]
+    int *s_rkey = reinterpret_cast<int *>(lds + a.ro_rkey);             // [LG]
+    int *s_rfl = reinterpret_cast<int *>(lds + a.ro_rfl);               // [LG]
+    float *s_dx = reinterpret_cast<float *>(lds + a.ro_dx);             // [P+1] dx by sorted row (+ a discard slot)
+    uint16_t *s_inv = reinterpret_cast<uint16_t *>(lds + a.ro_inv);     // [P] sorted row of each pair
 
     int g, c;
     if (!decode_tile(blockIdx.x, a.G, a.C, g, c)) return;
     const int f0 = g * FS;
     const int nfh = min(FS, F - f0);
-    const int64_t n_begin = static_cast<int64_t>(c) * a.NC;
-    const int64_t n_end = min(a.N, n_begin + a.NC);
-    if (n_begin >= n_end) return;
+    const int t_begin = c * a.SPC;
+    const int t_end = min(a.T, t_begin + a.SPC);
+    if (t_begin >= t_end) return;
     const int tid = threadIdx.x;
-    const int wave = tid / kWave;
-    const int lane = tid % kWave;
+    const int PM = a.PM;
 
-    // pair inputs of a sub-tile, prefetched into registers one sub-tile ahead:
-    // thread -> pairs i = tid + u * kBlock, i -> (sample i / FS, feature i % FS)
-    int pk[kPairsPerThread];
-    float pv[kPairsPerThread];
-    auto fetch_pairs = [&](int64_t sub) __attribute__((always_inline)) {
-        const int64_t ns = min(static_cast<int64_t>(NT), n_end - sub);
-#pragma unroll
-        for (int u = 0; u < kPairsPerThread; ++u) {
-            const int i = tid + u * kBlock;
-            const int s = i / FS;
-            const int fl = i - s * FS;
-            // unconditional loads (pair 0 stands in for padding) keep the
-            // wait for them a single counted one
-            const int64_t pair = (s < ns && fl < nfh) ? (sub + s) * F + f0 + fl : 0;
-            pk[u] = load_idx<IdxT>(a.idx, pair);
-            pv[u] = a.x[pair];
-        }
-    };
-    fetch_pairs(n_begin);
+    // The next sub-tile's descriptors, pieces and piece count travel in
+    // registers while the current one is reduced (kP / 2 / kBlock == 2 uint4
+    // of descriptors per thread; kPieceRegs piece entries, the ones past the
+    // capacity re-read entry 0 and are never stored).
+    static_assert(kP / 2 / kBlock == 2 && kPieceRegs == 5, "prefetch registers");
+    uint4 pd0, pd1;
+    uint32_t pp0, pp1, pp2, pp3, pp4;
+    int pnpc;
+#define PLE_PREFETCH(T_)                                                                         \
+    do {                                                                                         \
+        const int64_t tile_ = static_cast<int64_t>(T_) * a.G + g;                                \
+        const uint4 *src_ = reinterpret_cast<const uint4 *>(a.desc + tile_ * kP);                \
+        pd0 = src_[tid];                                                                         \
+        pd1 = src_[tid + kBlock];                                                                \
+        const uint32_t *ps_ = a.piece + tile_ * PM;                                              \
+        pp0 = ps_[tid < PM ? tid : 0];                                                           \
+        pp1 = ps_[tid + kBlock < PM ? tid + kBlock : 0];                                         \
+        pp2 = ps_[tid + 2 * kBlock < PM ? tid + 2 * kBlock : 0];                                 \
+        pp3 = ps_[tid + 3 * kBlock < PM ? tid + 3 * kBlock : 0];                                 \
+        pp4 = ps_[tid + 4 * kBlock < PM ? tid + 4 * kBlock : 0];                                 \
+        pnpc = a.npc[tile_];                                                                     \
+    } while (0)
+    PLE_PREFETCH(t_begin);
 
     // ---- stage tables, clear accumulators ---------------------------------
+    // Rows past a piece's end read the dummy row kP: q(frac) = +0 and sample
+    // NT, whose gradient offset lies past every sub-tile's span (zeros).
+    if (tid == 0) s_sdesc[kP] = make_uint2(0u, static_cast<uint32_t>(NT));
     for (int i = tid; i < FS; i += kBlock) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
-    for (int i = tid; i < FS * KB; i += kBlock) {
-        const int fl = i / KB;
-        s_edge[i] = fl < nfh ? a.edges[static_cast<int64_t>(f0) * KB + i] : 0.0f;
-    }
     for (int i = tid; i < FS * B; i += kBlock) {
         const int fl = i / B;
         s_iw[i] = fl < nfh ? a.iw[static_cast<int64_t>(f0) * B + i] : 0.0f;
@@ -182,122 +354,74 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
         }
         s_qw[i] = w;
     }
-    __syncthreads();
 
     const int lgw = LGW_T > 0 ? LGW_T : a.LGW;   // lanes per grad_output row (power of two)
-    const int LG = kBlock / lgw;                  // lane groups (slices) per workgroup
+    const int LG = kBlock / lgw;                  // lane groups (runs of pieces) per workgroup
     const int lg = tid / lgw;
     const int lc = tid - lg * lgw;
     const bool c_ok = lc < D / VEC;
-    const int R = kP / LG;                        // sorted rows per slice
-    const int NB = kP / kWave;                    // 64-pair blocks per sub-tile
-    const int NBf = NT / kWave;                   // blocks per feature
-    const int D2 = 2 * D, D3 = 3 * D;
+    const int D2 = 2 * D;
+    const int RS = kRawDb ? 3 * D : 2 * D;        // record stride {bucket | weighted (| raw g)}
+    const int nt_shift = __ffs(NT) - 1;           // NT is a power of two
 
-    for (int64_t sub = n_begin; sub < n_end; sub += NT) {
-        const int ns = static_cast<int>(min(static_cast<int64_t>(NT), n_end - sub));
-
-        // A. pair info, stored feature-major (p = fl * NT + s)
+    for (int t = t_begin; t < t_end; ++t) {
+        // the previous sub-tile's pieces are reduced and its records merged
+        reinterpret_cast<uint4 *>(s_sdesc)[tid] = pd0;
+        reinterpret_cast<uint4 *>(s_sdesc)[tid + kBlock] = pd1;
+        if (tid < PM) s_piece[tid] = pp0;
+        if (tid + kBlock < PM) s_piece[tid + kBlock] = pp1;
+        if (tid + 2 * kBlock < PM) s_piece[tid + 2 * kBlock] = pp2;
+        if (tid + 3 * kBlock < PM) s_piece[tid + 3 * kBlock] = pp3;
+        if (tid + 4 * kBlock < PM) s_piece[tid + 4 * kBlock] = pp4;
+        if (tid == 0) s_npc[0] = pnpc;
+        __syncthreads();
+        // (past the chunk's last sub-tile: the same sub-tile again, unused)
+        PLE_PREFETCH(t + 1 < t_end ? t + 1 : t);
+        // sorted row of each pair, for the dx stores (read after F's barrier)
 #pragma unroll
         for (int u = 0; u < kPairsPerThread; ++u) {
-            const int i = tid + u * kBlock;
-            const int s = i / FS;
-            const int fl = i - s * FS;
-            int key = B;
-            float qf = 0.0f;
-            if (s < ns && fl < nfh) {
-                const int k = clamp_bin(pk[u], s_nb[fl]);
-                const float v = pv[u];
-                const float e = s_edge[fl * KB + k];
-                qf = quant<Q>((v - e) * s_iw[fl * B + k]);
-                key = k | ((k > 0 && v == e) ? 0x8000 : 0);
-            }
-            s_info[fl * NT + s] = make_float2(qf, __int_as_float(key));
+            const int r = tid + u * kBlock;
+            const uint32_t y = s_sdesc[r].y;
+            s_inv[((y >> 24) << nt_shift) + (y & 0xffffff)] = static_cast<uint16_t>(r);
         }
-        for (int i = tid; i < NB * KB; i += kBlock) s_cnt[i] = 0;
-        __syncthreads();
+        const int64_t sub = static_cast<int64_t>(t) * NT;
+        const int ns = static_cast<int>(min(static_cast<int64_t>(NT), a.N - sub));
 
-        // B. rank of each pair among equal keys of its 64-pair block
-        for (int b = wave; b < NB; b += kWavesPerBlock) {
-            const int p = b * kWave + lane;
-            const int k = __float_as_int(s_info[p].y) & 0x7fff;
-            unsigned long long m = ~0ull;
-            for (int bit = 0; bit < a.nbits; ++bit) {
-                const bool set = (k >> bit) & 1;
-                const unsigned long long bal = __ballot(set);
-                m &= set ? bal : ~bal;
-            }
-            const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
-            const int rank = __popcll(m & lt);
-            s_rank[p] = static_cast<uint8_t>(rank);
-            if (rank == 0) s_cnt[b * KB + k] = static_cast<uint16_t>(__popcll(m));
-        }
-        __syncthreads();
-
-        // C. per key: prefix over the feature's blocks; totals -> segment starts
-        for (int kk = tid; kk < FS * KB; kk += kBlock) {
-            const int fl = kk / KB;
-            const int k = kk - fl * KB;
-            int run = 0;
-            for (int bb = 0; bb < NBf; ++bb) {
-                const int ci = (fl * NBf + bb) * KB + k;
-                const int cc = s_cnt[ci];
-                s_cnt[ci] = static_cast<uint16_t>(run);
-                run += cc;
-            }
-            s_seg[kk] = run;
-        }
-        __syncthreads();
-        block_exclusive_scan(s_seg, FS * KB, s_tmp);
-
-        // D. scatter: sorted position -> row descriptor {q(frac), key | edge | sample << 16}
-        for (int p = tid; p < kP; p += kBlock) {
-            const int fl = p / NT;
-            const int s = p - fl * NT;
-            const float2 inf = s_info[p];
-            const int kb = __float_as_int(inf.y);
-            const int k = kb & 0x7fff;
-            const int slot = s_seg[fl * KB + k] + s_cnt[(p / kWave) * KB + k] + s_rank[p];
-            s_sdesc[slot] = make_uint2(__float_as_uint(inf.x), static_cast<uint32_t>(kb & 0xffff) |
-                                                                (static_cast<uint32_t>(s) << 16));
-        }
-        __syncthreads();
-
-        // the next sub-tile's pair inputs travel while this one is reduced
-        if (sub + NT < n_end) fetch_pairs(sub + NT);
-
-        // F. slices of sorted rows, gradient rows prefetched a batch ahead
+        // F. pieces: lane group lg takes the contiguous pieces [j0, j1) (its
+        //    "run"), the next piece's gradient rows in flight while the
+        //    current one is reduced
         {
-            // Running sums of the slice's current key (feature, bin) -- packed as
-            // fl << 16 | k -- and, with rounding quantisation, of its feature.
-            // Padding rows (key B) and idle lanes (lc >= D / VEC) read a row of
-            // zeros, so they add nothing and need no masking.
+            // Running sums of the run's current key (feature, bin) -- packed as
+            // fl << 12 | k -- and, with rounding quantisation, of its feature.
+            // Rows past a piece's end and idle lanes (lc >= D / VEC) load from
+            // past the end of the gradient buffer, which reads zeros: they add
+            // nothing and need no masking.
             int cur = -1, db_fl = -1;
             bool first_key = true, first_fl = true;
             float ab[VEC], aw[VEC], ad[VEC];
 #pragma unroll
-            for (int t = 0; t < VEC; ++t) ab[t] = aw[t] = ad[t] = 0.0f;
+            for (int q = 0; q < VEC; ++q) ab[q] = aw[q] = ad[q] = 0.0f;
             if (lc == 0) {
                 s_rkey[lg] = -1;
                 s_rfl[lg] = -1;
             }
-            float *rec = s_rec + lg * D3 + lc * VEC;
+            float *rec = s_rec + lg * RS + lc * VEC;
 
-            // first key of the slice -> record; later keys -> straight into the
-            // histogram (this slice is their only writer).  One read-modify-write
-            // through a selected pointer keeps the code inlined per row small.
+            // first key of the run -> record; later keys -> straight into the
+            // histogram (this run is their only writer).  One read-modify-write
+            // through a selected pointer keeps the code inlined per piece small.
             auto flush_key = [&]() __attribute__((always_inline)) {
-                if (cur < 0 || (cur & 0xffff) >= B) return;
-                float *h = s_hist + (static_cast<size_t>(cur >> 16) * B + (cur & 0xffff)) * D2 + lc * VEC;
+                if (cur < 0) return;
+                float *h = s_hist + __umul24(__umul24(cur >> 12, B) + (cur & 0xfff), D2) + lc * VEC;
                 float *dst = first_key ? rec : h;
                 if (c_ok) {
                     float ob[VEC], ow[VEC];
                     lds_load_vec<VEC>(dst, ob);
                     lds_load_vec<VEC>(dst + D, ow);
 #pragma unroll
-                    for (int t = 0; t < VEC; ++t) {
-                        ob[t] = first_key ? ab[t] : ob[t] + ab[t];
-                        ow[t] = first_key ? aw[t] : ow[t] + aw[t];
+                    for (int q = 0; q < VEC; ++q) {
+                        ob[q] = first_key ? ab[q] : ob[q] + ab[q];
+                        ow[q] = first_key ? aw[q] : ow[q] + aw[q];
                     }
                     lds_store_vec<VEC>(dst, ob);
                     lds_store_vec<VEC>(dst + D, ow);
@@ -312,177 +436,185 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_fused_kernel(BwdArgs a) {
                     float o[VEC];
                     lds_load_vec<VEC>(dst, o);
 #pragma unroll
-                    for (int t = 0; t < VEC; ++t) o[t] = first_fl ? ad[t] : o[t] + ad[t];
+                    for (int q = 0; q < VEC; ++q) o[q] = first_fl ? ad[q] : o[q] + ad[q];
                     lds_store_vec<VEC>(dst, o);
                 }
                 if (first_fl && lc == 0) s_rfl[lg] = db_fl;
                 first_fl = false;
             };
 
-            // sorted position r -> feature r / NT (NT is a power of two)
-            const int nt_shift = __ffs(NT) - 1;
-            float gA[kUB][VEC], gB[kUB][VEC];
+            const int NPc = s_npc[0];
+            const int m = (NPc + LG - 1) / LG;           // pieces per run
+            const int j0 = lg * m;
+            const int j1 = min(j0 + m, NPc);
 
-            // gradient rows of this sub-tile: 32-bit element offsets from the
-            // sub-tile's first pair (the planner keeps NT * F * D below 2^31)
-            const char *gsub = static_cast<const char *>(a.g) +
-                               ((sub * F + f0) * D) * static_cast<int64_t>(GD == PLE_DTYPE_F32 ? 4 : 2);
-            const int rowF = F * D;
+            // The sub-tile's gradient rows as one buffer resource: byte offset
+            // s * rowFb + fl * Db + lane offset (24-bit products: the planner
+            // keeps the sub-tile's span below 2^31 bytes).  Offset `span`
+            // (first byte past the sub-tile) stands in for rows past a piece's
+            // end and for idle lanes.
+            constexpr uint32_t esz = GD == PLE_DTYPE_F32 ? 4 : 2;
+            const uint32_t rowFb = static_cast<uint32_t>(F) * D * esz;
+            const uint32_t Db = static_cast<uint32_t>(D) * esz;
+            const uint32_t span = static_cast<uint32_t>(ns) * rowFb;
+            const __amdgpu_buffer_rsrc_t grs = make_rsrc(
+                static_cast<const char *>(a.g) + (sub * F + f0) * static_cast<int64_t>(D) * esz, span);
+            // idle lanes: an offset past every span
+            const uint32_t laneoff = c_ok ? static_cast<uint32_t>(lc) * VEC * esz : 0x80000000u;
 
-            auto issue = [&](int rb, float (&gv)[kUB][VEC]) __attribute__((always_inline)) {
+            // Piece t of the run: its entry, its rows' descriptors, and loads
+            // of their gradient rows.  Past j1 the piece is empty (all rows
+            // read zeros).  Every lane loads, with no branch around the load,
+            // so each piece has one counted wait.
+            auto issue = [&](int tt, float (&gv)[kL][VEC], uint2 (&dv)[kL], uint32_t &pe) __attribute__((always_inline)) {
+                const int j = j0 + tt;
+                const bool real = j < j1;
+                pe = s_piece[real ? j : 0];
+                const int rs = static_cast<int>((pe >> 16) & 0xfff);
+                const int n = real ? static_cast<int>(pe >> 28) + 1 : 0;
+                const uint32_t flb = __umul24((pe >> 12) & 0xf, Db) + laneoff;
 #pragma unroll
-                for (int u = 0; u < kUB; ++u) {
-                    const int r = rb + u;
-                    const int fl = r >> nt_shift;
-                    const uint32_t dw = s_sdesc[r].y;
-                    const int s = static_cast<int>(dw >> 16);
-                    // every lane loads, with no branch around the load (so the
-                    // compiler waits for each batch separately); padding rows
-                    // and idle lanes load zeros
-                    const bool ok = c_ok && static_cast<int>(dw & 0x7fff) < B;
-                    const void *src = ok ? static_cast<const void *>(gsub) : static_cast<const void *>(g_zero_row);
-                    const int at = ok ? s * rowF + fl * D + lc * VEC : 0;
-                    load_grad_vec<GD, VEC>(src, at, gv[u]);   // 16-bit zeros decode to +0 too
-                }
+                for (int i = 0; i < kL; ++i) dv[i] = s_sdesc[i < n ? rs + i : kP];
+                // (the 24-bit product ignores the feature bits of .y)
+#pragma unroll
+                for (int i = 0; i < kL; ++i) load_grad_buf<GD, VEC>(grs, __umul24(dv[i].y, rowFb) + flb, gv[i]);
             };
 
-            // weight row and inverse width of the current key, reloaded from LDS
-            // when the key changes (idle lanes read column 0; their g is 0)
+            // weight rows k and k-1 and their inverse widths for the current
+            // key, reloaded from LDS when the key changes (idle lanes read
+            // column 0; their g is 0); row k-1 serves rows with x on e_k
             const int lcx = c_ok ? lc : 0;
-            float wk[VEC];
-            float iwk = 0.0f;
+            float wk[VEC], wp[VEC];
+            float iwk = 0.0f, iwp = 0.0f;
 #pragma unroll
-            for (int t = 0; t < VEC; ++t) wk[t] = 0.0f;
-            auto process = [&](int rb, const float (&gv)[kUB][VEC]) __attribute__((always_inline)) {
-                uint2 dsc[kUB];
+            for (int q = 0; q < VEC; ++q) wk[q] = wp[q] = 0.0f;
+            auto process = [&](int tt, const float (&gv)[kL][VEC], const uint2 (&dsc)[kL], uint32_t pe) __attribute__((always_inline)) {
+                const bool real = j0 + tt < j1;
+                const int n = real ? static_cast<int>(pe >> 28) + 1 : 0;
+                const int key = real ? static_cast<int>(pe & 0xffff) : cur;
+                const int fl = key >> 12;
+                if (key != cur) {
+                    flush_key();
 #pragma unroll
-                for (int u = 0; u < kUB; ++u) dsc[u] = s_sdesc[rb + u];
+                    for (int q = 0; q < VEC; ++q) ab[q] = aw[q] = 0.0f;
+                    if constexpr (kRawDb) {
+                        if (fl != db_fl) {
+                            flush_fl();
 #pragma unroll
-                for (int u = 0; u < kUB; ++u) {
-                    const int r = rb + u;
-                    const int fl = r >> nt_shift;
-                    const float qf = __uint_as_float(dsc[u].x);
-                    const uint32_t dw = dsc[u].y;
-                    const int k = static_cast<int>(dw & 0x7fff);
-                    const int s = static_cast<int>(dw >> 16);
-                    const int key = (fl << 16) | k;
-                    if (key != cur) {
-                        flush_key();
-#pragma unroll
-                        for (int t = 0; t < VEC; ++t) ab[t] = aw[t] = 0.0f;
-                        if constexpr (kRawDb) {
-                            if (fl != db_fl) {
-                                flush_fl();
-#pragma unroll
-                                for (int t = 0; t < VEC; ++t) ad[t] = 0.0f;
-                                db_fl = fl;
-                            }
+                            for (int q = 0; q < VEC; ++q) ad[q] = 0.0f;
+                            db_fl = fl;
                         }
-                        cur = key;
-                        const int kr = k < B ? k : 0;   // padding: any row (its g is 0)
-                        lds_load_vec<VEC>(s_qw + (static_cast<size_t>(fl) * B + kr) * D + lcx * VEC, wk);
-                        iwk = s_iw[fl * B + kr];
                     }
-                    float gq[VEC];
-                    float dot = 0.0f;
+                    cur = key;
+                    const int k = key & 0xfff;
+                    const int kp = k > 0 ? k - 1 : 0;
+                    const int rowbase = __umul24(fl, B);
+                    lds_load_vec<VEC>(s_qw + __umul24(rowbase + k, D) + lcx * VEC, wk);
+                    lds_load_vec<VEC>(s_qw + __umul24(rowbase + kp, D) + lcx * VEC, wp);
+                    iwk = s_iw[rowbase + k];
+                    iwp = s_iw[rowbase + kp];
+                }
+                const int rs = static_cast<int>((pe >> 16) & 0xfff);
 #pragma unroll
-                    for (int t = 0; t < VEC; ++t) {
-                        gq[t] = quant<Q>(gv[u][t]);
-                        ab[t] += gq[t];
-                        aw[t] = fmaf(qf, gq[t], aw[t]);
-                        if constexpr (kRawDb) ad[t] += gv[u][t];
-                        dot = fmaf(gq[t], wk[t], dot);
+                for (int i = 0; i < kL; ++i) {
+                    const float qf = __uint_as_float(dsc[i].x);
+                    float gq[VEC];
+                    float dot = 0.0f, dot2 = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < VEC; ++q) {
+                        gq[q] = quant<Q>(gv[i][q]);
+                        ab[q] += gq[q];
+                        aw[q] = fmaf(qf, gq[q], aw[q]);
+                        if constexpr (kRawDb) ad[q] += gv[i][q];
+                        dot = fmaf(gq[q], wk[q], dot);
+                        dot2 = fmaf(gq[q], wp[q], dot2);
                     }
                     float part = dot * iwk;
-                    if (dw & 0x8000) {                      // x on the bin's left edge (k >= 1)
-                        float wp[VEC];
-                        lds_load_vec<VEC>(s_qw + (static_cast<size_t>(fl) * B + k - 1) * D + lcx * VEC, wp);
-                        float dot2 = 0.0f;
-#pragma unroll
-                        for (int t = 0; t < VEC; ++t) dot2 = fmaf(gq[t], wp[t], dot2);
-                        part = fmaf(dot2, s_iw[fl * B + k - 1], part);
-                    }
+                    // x on the bin's left edge (k >= 1): the lower bin's term too
+                    part = dsc[i].x == 0x80000000u ? fmaf(dot2, iwp, part) : part;
                     if constexpr (LGW_T > 0) part = group_sum<LGW_T>(part);
                     else part = group_sum_rt(part, lgw);
-                    if (lc == 0) s_dx[(fl << nt_shift) + s] = part;
+                    // dx into LDS by sorted row (every lane of the group holds
+                    // the same sum; rows past the piece's end: the discard slot)
+                    s_dx[i < n ? rs + i : kP] = part;
                 }
             };
 
-            // Two register buffers: batch b+1 is in flight while batch b is
-            // reduced.  Every issue is unconditional (the one after the last
-            // batch re-reads the slice's first rows and is discarded), so the
-            // loop carries the same loads on every path and the waits stay
-            // per batch.
-            const int r0 = lg * R;
-            const int r1 = r0 + R;
-            if (R >= 2 * kUB) {
-                issue(r0, gA);
-                for (int rb = r0; rb < r1; rb += 2 * kUB) {
-                    issue(rb + kUB, gB);
-                    process(rb, gA);
-                    issue(rb + 2 * kUB < r1 ? rb + 2 * kUB : r0, gA);
-                    process(rb + kUB, gB);
+            // Two register buffers: piece t+1 is in flight while piece t is
+            // reduced.  m is the same for every run, so the loop is uniform;
+            // a piece issued past m is empty.
+            float gA[kL][VEC], gB[kL][VEC];
+            uint2 dA[kL], dB[kL];
+            uint32_t pA = 0, pB = 0;
+            if (m > 0) {
+                issue(0, gA, dA, pA);
+                int tt = 0;
+#pragma unroll 1
+                for (; tt + 1 < m; tt += 2) {
+                    issue(tt + 1, gB, dB, pB);
+                    process(tt, gA, dA, pA);
+                    issue(tt + 2, gA, dA, pA);
+                    process(tt + 1, gB, dB, pB);
                 }
-            } else {
-                for (int rb = r0; rb < r1; rb += kUB) {
-                    issue(rb, gA);
-                    process(rb, gA);
-                }
+                if (tt < m) process(tt, gA, dA, pA);
             }
             flush_key();
             if constexpr (kRawDb) flush_fl();
         }
         __syncthreads();
 
-        // G. slice records, one run of equal keys (features) per head, in order
+        // H. dx of the sub-tile, feature-major: coalesced stores
+        if (a.dxt) {
+#pragma unroll
+            for (int u = 0; u < kPairsPerThread; ++u) {
+                const int p = tid + u * kBlock;
+                const int fl = p / NT;
+                const int sidx = p - fl * NT;
+                if (fl < nfh && sidx < ns) a.dxt[static_cast<int64_t>(f0 + fl) * a.N + sub + sidx] = s_dx[s_inv[p]];
+            }
+        }
+
+        // G. run records, one run of equal keys (features) per head, in order
         if (c_ok) {
             const int key = s_rkey[lg];
             if (key >= 0 && (lg == 0 || s_rkey[lg - 1] != key)) {
                 float sb[VEC], sw[VEC];
 #pragma unroll
-                for (int t = 0; t < VEC; ++t) sb[t] = sw[t] = 0.0f;
+                for (int q = 0; q < VEC; ++q) sb[q] = sw[q] = 0.0f;
                 for (int j = lg; j < LG && s_rkey[j] == key; ++j) {
-                    const float *rj = s_rec + j * D3 + lc * VEC;
+                    const float *rj = s_rec + j * RS + lc * VEC;
 #pragma unroll
-                    for (int t = 0; t < VEC; ++t) {
-                        sb[t] += rj[t];
-                        sw[t] += rj[D + t];
+                    for (int q = 0; q < VEC; ++q) {
+                        sb[q] += rj[q];
+                        sw[q] += rj[D + q];
                     }
                 }
-                float *h = s_hist + (static_cast<size_t>(key >> 16) * B + (key & 0xffff)) * D2 + lc * VEC;
+                float *h = s_hist + (static_cast<size_t>(key >> 12) * B + (key & 0xfff)) * D2 + lc * VEC;
 #pragma unroll
-                for (int t = 0; t < VEC; ++t) {
-                    h[t] += sb[t];
-                    h[D + t] += sw[t];
+                for (int q = 0; q < VEC; ++q) {
+                    h[q] += sb[q];
+                    h[D + q] += sw[q];
                 }
             }
             const int rfl = kRawDb ? s_rfl[lg] : -1;
             if (rfl >= 0 && (lg == 0 || s_rfl[lg - 1] != rfl)) {
                 float sd[VEC];
 #pragma unroll
-                for (int t = 0; t < VEC; ++t) sd[t] = 0.0f;
+                for (int q = 0; q < VEC; ++q) sd[q] = 0.0f;
                 for (int j = lg; j < LG && s_rfl[j] == rfl; ++j) {
-                    const float *rj = s_rec + j * D3 + D2 + lc * VEC;
+                    const float *rj = s_rec + j * RS + D2 + lc * VEC;
 #pragma unroll
-                    for (int t = 0; t < VEC; ++t) sd[t] += rj[t];
+                    for (int q = 0; q < VEC; ++q) sd[q] += rj[q];
                 }
 #pragma unroll
-                for (int t = 0; t < VEC; ++t) s_db[rfl * D + lc * VEC + t] += sd[t];
+                for (int q = 0; q < VEC; ++q) s_db[rfl * D + lc * VEC + q] += sd[q];
             }
         }
-
-        // H. dx, coalesced along the group's features
-        if (a.dx) {
-#pragma unroll
-            for (int u = 0; u < kPairsPerThread; ++u) {
-                const int i = tid + u * kBlock;
-                const int s = i / FS;
-                const int fl = i - s * FS;
-                if (s < ns && fl < nfh) a.dx[(sub + s) * F + f0 + fl] = s_dx[fl * NT + s];
-            }
-        }
-        __syncthreads();
+        // (the next iteration's barrier orders these histogram updates before
+        // its pieces)
     }
+#undef PLE_PREFETCH
+    __syncthreads();
 
     // chunk partials
     if (a.part) {
@@ -617,52 +749,119 @@ __global__ __launch_bounds__(kWave) void ple_bwd_simple_hist_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// finalize: one workgroup per feature
+// finalize: one workgroup per (feature, group of kFinCols columns)
 // ---------------------------------------------------------------------------
 
-// Sums the chunk partials of every (bin, column) in chunk order into LDS,
-// then one lane per column takes the suffix over logical bins:
-// dW[phys(k)] = weighted[k] + sum_{m>k} bucket[m]; slots no bin maps to get
-// 0.  The bias gradient sums its chunk partials in chunk order.
+constexpr int kFinCols = 8;
+
+// Sums the chunk partials of every (bin, column) of the group in chunk order
+// into LDS (every thread's loads issued together), then one lane per column
+// takes the suffix over logical bins: dW[phys(k)] = weighted[k] +
+// sum_{m>k} bucket[m]; slots no bin maps to get 0.  The bias gradient is the
+// sum of the buckets (fp32 gradients) or of its own chunk partials.
 __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
-    extern __shared__ float tot[];       // [n][2D]
+    extern __shared__ float tot[];       // [n][2][kFinCols]
     const int f = blockIdx.x;
+    const int j0 = blockIdx.y * kFinCols;
     const int B = a.B, D = a.D, F = a.F;
     const int D2 = 2 * D;
+    const int nc = min(kFinCols, D - j0);
     const int n = clamp_nbins(a.nbins[f], B);
     const int tid = threadIdx.x;
     const int64_t cstride = static_cast<int64_t>(F) * B * D2;
     const float *src = a.part + static_cast<int64_t>(f) * B * D2;
-    const bool need_tot = a.dw || (a.db && a.db_from_buckets);
+    const bool need_tot = !a.fin_direct && (a.dw || (a.db && a.db_from_buckets));
+    // bin k's chunk sum of half h (0: bucket, 1: weighted) for this thread's column
+    auto total = [&](int k, int h) {
+        if (!a.fin_direct) return tot[(k * 2 + h) * kFinCols + tid];
+        const float *p = src + k * D2 + h * D + j0 + tid;
+        float s = 0.0f;
+        for (int cc = 0; cc < a.Cd; ++cc) s += p[cc * cstride];
+        return s;
+    };
     if (need_tot) {
-        for (int i = tid; i < n * D2; i += kBlock) {
+        // element e -> (bin k, half h: bucket / weighted, column j0 + c)
+        for (int e = tid; e < n * 2 * kFinCols; e += kBlock) {
+            const int k = e / (2 * kFinCols);
+            const int h = (e / kFinCols) & 1;
+            const int cidx = e % kFinCols;
             float s = 0.0f;
+            if (cidx < nc) {
+                const float *p = src + k * D2 + h * D + j0 + cidx;
 #pragma unroll 8
-            for (int cc = 0; cc < a.Cd; ++cc) s += src[cc * cstride + i];
-            tot[i] = s;
+                for (int cc = 0; cc < a.Cd; ++cc) s += p[cc * cstride];
+            }
+            tot[e] = s;
         }
         __syncthreads();
     }
-    if (a.dw) {
-        for (int j = tid; j < D; j += kBlock) {
+    if (tid < nc) {
+        const int j = j0 + tid;
+        if (a.dw) {
             float fut = 0.0f;
             for (int k = n - 1; k >= 0; --k) {
-                a.dw[(static_cast<int64_t>(f) * B + phys_bin(k, n, B)) * D + j] = tot[k * D2 + D + j] + fut;
-                fut += tot[k * D2 + j];
+                a.dw[(static_cast<int64_t>(f) * B + phys_bin(k, n, B)) * D + j] = total(k, 1) + fut;
+                fut += total(k, 0);
+            }
+            for (int k = n - 1; k < B - 1; ++k) a.dw[(static_cast<int64_t>(f) * B + k) * D + j] = 0.0f;
+        }
+        if (a.db) {
+            float sb = 0.0f;
+            if (a.db_from_buckets) {
+                for (int k = n - 1; k >= 0; --k) sb += total(k, 0);
+            } else {
+                for (int cc = 0; cc < a.Cd; ++cc) sb += a.part_db[(static_cast<int64_t>(cc) * F + f) * D + j];
+            }
+            a.db[static_cast<int64_t>(f) * D + j] = sb;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dx: feature-major [F][N] -> [N][F]
+// ---------------------------------------------------------------------------
+
+constexpr int kTr = 64;   // transpose tile (samples x features)
+
+// V4: 16-byte loads along samples and stores along features (N and F
+// multiples of 4); otherwise one element per access.
+template <bool V4>
+__global__ __launch_bounds__(kBlock) void ple_bwd_dx_transpose_kernel(const float *__restrict__ src, float *__restrict__ dst,
+                                                                   int64_t N, int F) {
+    __shared__ float tile[kTr][kTr + 1];   // [feature][sample]
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kTr;
+    const int f0 = blockIdx.y * kTr;
+    const int tid = threadIdx.x;
+    if constexpr (V4) {
+        const int c4 = tid % (kTr / 4);
+        for (int r = tid / (kTr / 4); r < kTr; r += kBlock / (kTr / 4)) {
+            const int f = f0 + r;
+            const int64_t n = n0 + 4 * c4;
+            if (f < F && n < N) {
+                const float4 v = *reinterpret_cast<const float4 *>(src + static_cast<int64_t>(f) * N + n);
+                tile[r][4 * c4] = v.x; tile[r][4 * c4 + 1] = v.y; tile[r][4 * c4 + 2] = v.z; tile[r][4 * c4 + 3] = v.w;
             }
         }
-        for (int i = tid; i < (B - n) * D; i += kBlock)
-            a.dw[(static_cast<int64_t>(f) * B + (n - 1) + i / D) * D + i % D] = 0.0f;
-    }
-    if (a.db) {
-        for (int j = tid; j < D; j += kBlock) {
-            float s = 0.0f;
-            if (a.db_from_buckets) {
-                for (int k = n - 1; k >= 0; --k) s += tot[k * D2 + j];
-            } else {
-                for (int cc = 0; cc < a.Cd; ++cc) s += a.part_db[(static_cast<int64_t>(cc) * F + f) * D + j];
-            }
-            a.db[static_cast<int64_t>(f) * D + j] = s;
+        __syncthreads();
+        for (int r = tid / (kTr / 4); r < kTr; r += kBlock / (kTr / 4)) {
+            const int64_t n = n0 + r;
+            const int f = f0 + 4 * c4;
+            if (f < F && n < N)
+                *reinterpret_cast<float4 *>(dst + n * F + f) =
+                    make_float4(tile[4 * c4][r], tile[4 * c4 + 1][r], tile[4 * c4 + 2][r], tile[4 * c4 + 3][r]);
+        }
+    } else {
+        const int tx = tid % kTr;
+        for (int r = tid / kTr; r < kTr; r += kBlock / kTr) {
+            const int f = f0 + r;
+            const int64_t n = n0 + tx;
+            if (f < F && n < N) tile[r][tx] = src[static_cast<int64_t>(f) * N + n];
+        }
+        __syncthreads();
+        for (int r = tid / kTr; r < kTr; r += kBlock / kTr) {
+            const int64_t n = n0 + r;
+            const int f = f0 + tx;
+            if (f < F && n < N) dst[n * F + f] = tile[tx][r];
         }
     }
 }
@@ -672,7 +871,9 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 
 constexpr size_t kPartialBudget = 64ull << 20;   // bytes of chunk partials
-constexpr size_t kFusedLdsTwoPerCu = 80 * 1024;
+// LDS per reduce workgroup the planner aims for: two workgroups per CU (the
+// kernel's registers allow two waves per SIMD)
+constexpr size_t kReduceLdsTarget = 80 * 1024;
 
 int env_int(const char *name, int dflt) {
     const char *s = getenv(name);
@@ -681,53 +882,78 @@ int env_int(const char *name, int dflt) {
 }
 
 struct BwdPlan {
-    bool fused;
+    bool sorted;
     int vec;
     int C, Cd;
     int64_t NC;
-    size_t lds;
-    size_t part_bytes, part_db_bytes;
-    BwdArgs geo;     // fused geometry and LDS offsets
-    size_t total() const { return align_up(part_bytes, 256) + align_up(part_db_bytes, 256); }
+    size_t lds, sort_lds;
+    size_t part_bytes, part_db_bytes, desc_bytes, piece_bytes, npc_bytes, dxt_bytes;
+    BwdArgs geo;     // sorted-path geometry and LDS offsets
+    size_t total() const {
+        return align_up(part_bytes, 256) + align_up(part_db_bytes, 256) + align_up(desc_bytes, 256) +
+               align_up(piece_bytes, 256) + align_up(npc_bytes, 256) + align_up(dxt_bytes, 256);
+    }
 };
 
-size_t fused_layout(BwdArgs &g, int FS, int P, int B, int D, int LG) {
+struct LdsTaker {
     size_t off = 0;
-    auto take = [&](int &field, size_t bytes) {
+    void operator()(int &field, size_t bytes) {
         field = static_cast<int>(off);
         off = align_up(off + bytes, 16);
-    };
+    }
+};
+
+size_t sort_layout(BwdArgs &g, int FS, int B, int PM) {
+    LdsTaker take;
     const size_t KB = static_cast<size_t>(B) + 1;
-    take(g.o_qw, 4ull * FS * B * D);
-    take(g.o_hist, 8ull * FS * B * D);
-    take(g.o_db, 4ull * FS * D);
-    take(g.o_edge, 4ull * FS * KB);
-    take(g.o_iw, 4ull * FS * B);
-    take(g.o_nb, 4ull * FS);
-    take(g.o_info, 8ull * P);
-    take(g.o_order, 8ull * P);
-    take(g.o_rank, 1ull * P);
-    take(g.o_cnt, 2ull * (P / kWave) * KB);
-    take(g.o_seg, 4ull * (FS * KB + 1));
-    take(g.o_dx, 4ull * P);
-    take(g.o_rec, 12ull * LG * D);
-    take(g.o_rkey, 4ull * LG);
-    take(g.o_rfl, 4ull * LG);
-    take(g.o_tmp, 4ull * kWavesPerBlock);
-    return off;
+    take(g.so_nb, 4ull * FS);
+    take(g.so_edge, 4ull * FS * KB);
+    take(g.so_iw, 4ull * FS * B);
+    take(g.so_info, 8ull * kP);
+    take(g.so_rank, 1ull * kP);
+    take(g.so_cnt, 2ull * (kP / kWave) * KB);
+    take(g.so_seg, 4ull * (FS * KB + 1));
+    take(g.so_tmp, 4ull * kWavesPerBlock);
+    take(g.so_desc, 8ull * kP);
+    take(g.so_piece, 4ull * PM);
+    return take.off;
+}
+
+// raw_db: records carry the raw-gradient bias sums too (quantised gradients)
+size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_db) {
+    LdsTaker take;
+    take(g.ro_qw, 4ull * FS * B * D);
+    take(g.ro_hist, 8ull * FS * B * D);
+    take(g.ro_db, 4ull * FS * D);
+    take(g.ro_iw, 4ull * FS * B);
+    take(g.ro_nb, 4ull * FS);
+    take(g.ro_desc, 8ull * (kP + 1));
+    take(g.ro_piece, 4ull * PM);
+    take(g.ro_npc, 4);
+    take(g.ro_rec, (raw_db ? 12ull : 8ull) * LG * D);
+    take(g.ro_rkey, 4ull * LG);
+    take(g.ro_rfl, 4ull * LG);
+    take(g.ro_dx, 4ull * (kP + 1));
+    take(g.ro_inv, 2ull * kP);
+    return take.off;
 }
 
 // g_align16: the gradient's base address is 16-byte aligned
-BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16) {
+BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16, bool raw_db) {
     BwdPlan pl{};
     const int cus = device_cu_count();
-    pl.fused = false;
-    // fused geometry: VEC=4 rows of D/4 lanes when D allows, else one column
-    // per lane; lane groups of a power-of-two width between 2 and 64
-    if (B <= 4096 && static_cast<int64_t>(kP) * F * D < INT32_MAX && env_int("PLE_BWD_SIMPLE", 0) == 0) {
-        // 8 floats per lane when D allows (half the lanes, and half the per-row
-        // overhead, of 4 per lane)
-        const int vec = !g_align16 ? 1 : (D % 8 == 0 ? 8 : (D % 4 == 0 && D >= 8 ? 4 : 1));
+    pl.sorted = false;
+    // Sorted path: bins fit the 12-bit field of a piece, and a sub-tile's
+    // gradient rows span less than 2^31 bytes (32-bit buffer offsets).
+    if (B <= 4096 && static_cast<int64_t>(kP) * F * D * 4 < INT32_MAX && env_int("PLE_BWD_SIMPLE", 0) == 0) {
+        // 4 floats per lane (16-byte loads for fp32 gradients) when D allows:
+        // 8 per lane halves the per-row instructions but needs registers for
+        // two waves per SIMD only, which hides less latency; lane groups of a
+        // power-of-two width
+        int vec = !g_align16 ? 1 : (D % 4 == 0 ? 4 : 1);
+        const int vec_env = env_int("PLE_BWD_VEC", 0);    // tuning: 8 or 1 instead of the default
+        if (vec_env == 8 && D % 8 == 0 && g_align16) vec = 8;
+        if (vec_env == 1) vec = 1;
         const int uv = static_cast<int>(D / vec);
         int lgw = 2;
         while (lgw < uv) lgw *= 2;
@@ -736,11 +962,12 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
             int best_fs = 0;
             size_t best_lds = 0;
             BwdArgs geo{};
+            auto pm_for = [&](int fs) { return kP / kL + static_cast<int>(std::min<int64_t>(kP, fs * B)); };
             for (int fs = 4; fs >= 1; fs /= 2) {
                 if (fs > 1 && fs > F) continue;
                 BwdArgs t{};
-                const size_t lds = fused_layout(t, fs, kP, static_cast<int>(B), static_cast<int>(D), LG);
-                if (lds <= kFusedLdsTwoPerCu || (fs == 1 && lds <= kLdsMax)) {
+                const size_t lds = reduce_layout(t, fs, static_cast<int>(B), static_cast<int>(D), LG, pm_for(fs), raw_db);
+                if (lds <= kReduceLdsTarget || (fs == 1 && lds <= kLdsMax)) {
                     best_fs = fs;
                     best_lds = lds;
                     geo = t;
@@ -750,7 +977,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
             const int fs_env = env_int("PLE_BWD_FS", 0);
             if (fs_env == 1 || fs_env == 2 || fs_env == 4 || fs_env == 8 || fs_env == 16) {
                 BwdArgs t{};
-                const size_t lds = fused_layout(t, fs_env, kP, static_cast<int>(B), static_cast<int>(D), LG);
+                const size_t lds = reduce_layout(t, fs_env, static_cast<int>(B), static_cast<int>(D), LG, pm_for(fs_env), raw_db);
                 if (lds <= kLdsMax) {
                     best_fs = fs_env;
                     best_lds = lds;
@@ -758,34 +985,44 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                 }
             }
             if (best_fs > 0) {
-                pl.fused = true;
-                pl.vec = vec;
-                pl.lds = best_lds;
-                geo.FS = best_fs;
-                geo.G = static_cast<int>((F + best_fs - 1) / best_fs);
-                geo.P = kP;
-                geo.NT = kP / best_fs;
-                geo.LGW = lgw;
-                int nbits = 0;
-                while ((1ll << nbits) <= B) ++nbits;      // keys 0..B
-                geo.nbits = nbits;
-                pl.geo = geo;
-                const int64_t per_chunk = F * B * 2 * D * 4;
-                int64_t c = (static_cast<int64_t>(env_int("PLE_BWD_WG_PER_CU", 4)) * cus + geo.G - 1) / geo.G;
-                const int64_t budget_c = static_cast<int64_t>(kPartialBudget) / per_chunk;
-                if (c > budget_c) c = budget_c;
-                const int64_t max_c = (N + geo.NT - 1) / geo.NT;   // at least one sub-tile per chunk
-                if (c > max_c) c = max_c;
-                if (c < 1) c = 1;
-                int64_t nc = (N + c - 1) / c;
-                nc = (nc + geo.NT - 1) / geo.NT * geo.NT;
-                pl.NC = nc;
-                pl.Cd = static_cast<int>((N + nc - 1) / nc);
-                pl.C = (pl.Cd + kNumXcd - 1) / kNumXcd * kNumXcd;
+                const int PM = pm_for(best_fs);
+                const size_t slds = sort_layout(geo, best_fs, static_cast<int>(B), PM);
+                if (slds <= kLdsMax) {
+                    pl.sorted = true;
+                    pl.vec = vec;
+                    pl.lds = best_lds;
+                    pl.sort_lds = slds;
+                    geo.FS = best_fs;
+                    geo.G = static_cast<int>((F + best_fs - 1) / best_fs);
+                    geo.NT = kP / best_fs;
+                    geo.T = static_cast<int>((N + geo.NT - 1) / geo.NT);
+                    geo.PM = PM;
+                    geo.LGW = lgw;
+                    int nbits = 0;
+                    while ((1ll << nbits) <= B) ++nbits;      // keys 0..B
+                    geo.nbits = nbits;
+                    // chunks of sub-tiles: about PLE_BWD_WG_PER_CU reduce
+                    // workgroups per CU, within the partials budget
+                    const int64_t per_chunk = F * B * 2 * D * 4;
+                    int64_t c = (static_cast<int64_t>(env_int("PLE_BWD_WG_PER_CU", 4)) * cus + geo.G - 1) / geo.G;
+                    const int64_t budget_c = static_cast<int64_t>(kPartialBudget) / per_chunk;
+                    if (c > budget_c) c = budget_c;
+                    if (c > geo.T) c = geo.T;
+                    if (c < 1) c = 1;
+                    geo.SPC = static_cast<int>((geo.T + c - 1) / c);
+                    pl.C = pl.Cd = (geo.T + geo.SPC - 1) / geo.SPC;
+                    pl.NC = static_cast<int64_t>(geo.SPC) * geo.NT;
+                    pl.geo = geo;
+                    const int64_t tiles = static_cast<int64_t>(geo.T) * geo.G;
+                    pl.desc_bytes = static_cast<size_t>(tiles) * kP * sizeof(uint2);
+                    pl.piece_bytes = static_cast<size_t>(tiles) * PM * sizeof(uint32_t);
+                    pl.npc_bytes = static_cast<size_t>(tiles) * sizeof(int);
+                    pl.dxt_bytes = static_cast<size_t>(N) * F * sizeof(float);
+                }
             }
         }
     }
-    if (!pl.fused) {
+    if (!pl.sorted) {
         const int64_t waves = 32 * static_cast<int64_t>(cus);
         int64_t c = (waves + F - 1) / F;
         const int64_t per_chunk = F * B * 2 * D * 4;
@@ -804,44 +1041,53 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
     return pl;
 }
 
-// Bin indices are uint8 (up to 256 bins) or int16 (up to 32766 bins, the
-// largest key the fused sort encodes).
-template <int GD, int Q, int VEC, int LGW>
-hipError_t launch_fused_idx(const BwdArgs &a, int idxb, dim3 grid, size_t lds, hipStream_t s) {
-    if (idxb == 1) hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, VEC, LGW, uint8_t>), grid, dim3(kBlock), lds, s, a);
-    else hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, VEC, LGW, int16_t>), grid, dim3(kBlock), lds, s, a);
+// Bin indices are uint8 (up to 256 bins) or int16 (up to 32766 bins).
+template <int Q>
+hipError_t launch_sort(const BwdArgs &a, int idxb, dim3 grid, size_t lds, hipStream_t s) {
+    if (idxb == 1) hipLaunchKernelGGL((ple_bwd_sort_kernel<Q, uint8_t>), grid, dim3(kBlock), lds, s, a);
+    else hipLaunchKernelGGL((ple_bwd_sort_kernel<Q, int16_t>), grid, dim3(kBlock), lds, s, a);
     return hipGetLastError();
 }
 
-// Lane-group width as a template argument for the VEC=4 rows (DPP
+// Lane-group width as a template argument for the 8- and 4-float rows (DPP
 // reductions); the one-column-per-lane variant takes it at run time.
 template <int GD, int Q>
-hipError_t launch_fused(const BwdArgs &a, int vec, int idxb, dim3 grid, size_t lds, hipStream_t s) {
+hipError_t launch_reduce(const BwdArgs &a, int vec, dim3 grid, size_t lds, hipStream_t s) {
     if (vec == 8) {
         switch (a.LGW) {
-            case 2: return launch_fused_idx<GD, Q, 8, 2>(a, idxb, grid, lds, s);
-            case 4: return launch_fused_idx<GD, Q, 8, 4>(a, idxb, grid, lds, s);
-            default: return launch_fused_idx<GD, Q, 8, 8>(a, idxb, grid, lds, s);
+            case 2: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 2>), grid, dim3(kBlock), lds, s, a); break;
+            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 4>), grid, dim3(kBlock), lds, s, a); break;
+            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 8>), grid, dim3(kBlock), lds, s, a); break;
         }
-    }
-    if (vec == 4) {
+    } else if (vec == 4) {
         switch (a.LGW) {
-            case 4: return launch_fused_idx<GD, Q, 4, 4>(a, idxb, grid, lds, s);
-            case 8: return launch_fused_idx<GD, Q, 4, 8>(a, idxb, grid, lds, s);
-            default: return launch_fused_idx<GD, Q, 4, 16>(a, idxb, grid, lds, s);
+            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 4>), grid, dim3(kBlock), lds, s, a); break;
+            case 8: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 8>), grid, dim3(kBlock), lds, s, a); break;
+            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 16>), grid, dim3(kBlock), lds, s, a); break;
         }
+    } else {
+        hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 0>), grid, dim3(kBlock), lds, s, a);
     }
-    return launch_fused_idx<GD, Q, 1, 0>(a, idxb, grid, lds, s);
+    return hipGetLastError();
 }
 
 template <int GD, int Q>
 hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bool want_dwdb, hipStream_t s) {
     hipError_t e = hipSuccess;
-    if (pl.fused) {
+    if (pl.sorted) {
         a.db_from_buckets = Q == PLE_DTYPE_F32;
-        const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.G) * pl.C));
-        e = launch_fused<GD, Q>(a, pl.vec, idxb, grid, pl.lds, s);
+        e = launch_sort<Q>(a, idxb, dim3(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, a.T))), pl.sort_lds, s);
         if (e != hipSuccess) return e;
+        e = launch_reduce<GD, Q>(a, pl.vec, dim3(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, pl.C))), pl.lds, s);
+        if (e != hipSuccess) return e;
+        if (a.dxt) {
+            const dim3 tg(static_cast<unsigned>((a.N + kTr - 1) / kTr), static_cast<unsigned>((a.F + kTr - 1) / kTr));
+            const bool v4 = a.N % 4 == 0 && a.F % 4 == 0 && reinterpret_cast<uintptr_t>(a.dx) % 16 == 0;
+            if (v4) hipLaunchKernelGGL(ple_bwd_dx_transpose_kernel<true>, tg, dim3(kBlock), 0, s, a.dxt, a.dx, a.N, a.F);
+            else hipLaunchKernelGGL(ple_bwd_dx_transpose_kernel<false>, tg, dim3(kBlock), 0, s, a.dxt, a.dx, a.N, a.F);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
     } else {
         if (want_dx) {
             const int64_t pairs = a.N * a.F;
@@ -863,8 +1109,11 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
         }
     }
     if (want_dwdb) {
-        const size_t lds = static_cast<size_t>(a.B) * 2 * a.D * sizeof(float);
-        hipLaunchKernelGGL(ple_bwd_finalize_kernel, dim3(a.F), dim3(kBlock), lds, s, a);
+        size_t lds = static_cast<size_t>(a.B) * 2 * kFinCols * sizeof(float);
+        a.fin_direct = lds > kLdsMax;          // very many bins: no LDS table
+        if (a.fin_direct) lds = 0;
+        const dim3 fg(static_cast<unsigned>(a.F), static_cast<unsigned>((a.D + kFinCols - 1) / kFinCols));
+        hipLaunchKernelGGL(ple_bwd_finalize_kernel, fg, dim3(kBlock), lds, s, a);
         e = hipGetLastError();
     }
     return e;
@@ -889,10 +1138,14 @@ hipError_t launch_q(const BwdArgs &a, const BwdPlan &pl, int q, int idxb, bool w
 }  // namespace
 
 size_t backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D) {
-    // the plan depends on the gradient's alignment; report the largest need
-    const size_t a = plan_backward(N, F, B, D, true).total();
-    const size_t b = plan_backward(N, F, B, D, false).total();
-    return a > b ? a : b;
+    // the plan depends on the gradient's alignment and dtype; report the largest need
+    size_t need = 0;
+    for (int al = 0; al < 2; ++al)
+        for (int raw = 0; raw < 2; ++raw) {
+            const size_t t = plan_backward(N, F, B, D, al != 0, raw != 0).total();
+            need = t > need ? t : need;
+        }
+    return need;
 }
 
 int backward_run(const BackwardRequest &r) {
@@ -902,19 +1155,37 @@ int backward_run(const BackwardRequest &r) {
     const uintptr_t gaddr = reinterpret_cast<uintptr_t>(r.g);
     const int gbytes = r.grad_dtype == PLE_DTYPE_F32 ? 4 : 2;
     if (gaddr % gbytes != 0) return PLE_E_MISALIGNED;
-    BwdPlan pl = plan_backward(r.N, r.F, r.B, r.D, gaddr % 16 == 0);
-    if (!pl.fused && want_dwdb && pl.lds > kLdsMax) return PLE_E_UNSUPPORTED;
-    const size_t need = pl.total();
-    if (want_dwdb && (r.workspace == nullptr || r.workspace_bytes < need ||
-                      reinterpret_cast<uintptr_t>(r.workspace) % 256 != 0))
+    BwdPlan pl = plan_backward(r.N, r.F, r.B, r.D, gaddr % 16 == 0, r.quant != PLE_DTYPE_F32);
+    if (!pl.sorted && want_dwdb && pl.lds > kLdsMax) return PLE_E_UNSUPPORTED;
+    // the sorted path always needs its descriptors; the fallback only for dW / db
+    const size_t need = (pl.sorted || want_dwdb) ? pl.total() : 0;
+    if (need > 0 && (r.workspace == nullptr || r.workspace_bytes < need ||
+                     reinterpret_cast<uintptr_t>(r.workspace) % 256 != 0))
         return PLE_E_WORKSPACE;
-    if (static_cast<int64_t>(pl.fused ? pl.geo.G : r.F) * pl.C > INT32_MAX) return PLE_E_TOO_LARGE;
+    const int64_t grid_max = pl.sorted ? kNumXcd * std::max(tiles_per_xcd(pl.geo.G, pl.geo.T), tiles_per_xcd(pl.geo.G, pl.C))
+                                       : static_cast<int64_t>(r.F) * pl.C;
+    if (grid_max > INT32_MAX) return PLE_E_TOO_LARGE;
     BwdArgs a = pl.geo;
     a.g = r.g; a.x = r.x; a.edges = r.edges; a.iw = r.iw; a.nbins = r.nbins; a.weight = r.weight;
     a.idx = r.idx; a.dx = r.dx; a.dw = r.dw; a.db = r.db;
     char *ws = static_cast<char *>(r.workspace);
-    a.part = want_dwdb ? reinterpret_cast<float *>(ws) : nullptr;
-    a.part_db = want_dwdb ? reinterpret_cast<float *>(ws + align_up(pl.part_bytes, 256)) : nullptr;
+    size_t off = 0;
+    auto carve = [&](size_t bytes) {
+        char *p = ws + off;
+        off += align_up(bytes, 256);
+        return p;
+    };
+    float *part = reinterpret_cast<float *>(carve(pl.part_bytes));
+    float *part_db = reinterpret_cast<float *>(carve(pl.part_db_bytes));
+    a.part = want_dwdb ? part : nullptr;
+    a.part_db = want_dwdb ? part_db : nullptr;
+    if (pl.sorted) {
+        a.desc = reinterpret_cast<uint2 *>(carve(pl.desc_bytes));
+        a.piece = reinterpret_cast<uint32_t *>(carve(pl.piece_bytes));
+        a.npc = reinterpret_cast<int *>(carve(pl.npc_bytes));
+        float *dxt = reinterpret_cast<float *>(carve(pl.dxt_bytes));
+        a.dxt = want_dx ? dxt : nullptr;
+    }
     a.N = r.N; a.F = static_cast<int>(r.F); a.B = static_cast<int>(r.B); a.D = static_cast<int>(r.D);
     a.C = pl.C; a.Cd = pl.Cd; a.NC = pl.NC;
     const int idxb = idx_bytes_for(r.B);

@@ -105,6 +105,58 @@ __device__ __forceinline__ void load_grad_vec(const void *p, int64_t i, float *o
     }
 }
 
+// Buffer resource over `bytes` bytes at `base` (raw addressing, stride 0).
+// Loads at byte offsets at or beyond `bytes` return zeros.  Both arguments
+// must be wave-uniform; they pass through readfirstlane so the compiler
+// keeps the resource in scalar registers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t p = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32));
+    void *pu = reinterpret_cast<void *>((static_cast<uint64_t>(hi) << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(pu, static_cast<short>(0),
+                                             static_cast<int>(__builtin_amdgcn_readfirstlane(bytes)), 0x00020000);
+}
+
+// VEC consecutive gradient elements at byte offset `off` of a buffer
+// resource, as floats (VEC in {1, 2, 4, 8}; `off` aligned for the access).
+template <int G, int VEC>
+__device__ __forceinline__ void load_grad_buf(__amdgpu_buffer_rsrc_t rs, uint32_t off, float *out) {
+    if constexpr (G == PLE_DTYPE_F32) {
+        if constexpr (VEC >= 4) {
+#pragma unroll
+            for (int q = 0; q < VEC / 4; ++q) {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * q, 0, 0);
+                out[4 * q] = __uint_as_float(v[0]); out[4 * q + 1] = __uint_as_float(v[1]);
+                out[4 * q + 2] = __uint_as_float(v[2]); out[4 * q + 3] = __uint_as_float(v[3]);
+            }
+        } else if constexpr (VEC == 2) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+            out[0] = __uint_as_float(v[0]); out[1] = __uint_as_float(v[1]);
+        } else {
+            out[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+        }
+    } else {
+        uint32_t w[VEC / 2 > 0 ? VEC / 2 : 1];
+        if constexpr (VEC == 8) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+            w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+        } else if constexpr (VEC == 4) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+            w[0] = v[0]; w[1] = v[1];
+        } else if constexpr (VEC == 2) {
+            w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+        } else {
+            w[0] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < VEC; ++t) {
+            const uint16_t h = static_cast<uint16_t>(w[t / 2] >> (16 * (t % 2)));
+            out[t] = (G == PLE_DTYPE_BF16) ? bf16_to_float(h) : f16_to_float(h);
+        }
+    }
+}
+
 // VEC consecutive floats from / to LDS (16-byte accesses for VEC 4 and 8;
 // the address is 16-byte aligned in those cases).
 template <int VEC>
@@ -228,16 +280,26 @@ __device__ __forceinline__ int load_idx(const void *p, int64_t i) {
     return static_cast<int>(static_cast<const IdxT *>(p)[i]);
 }
 
-// Workgroup -> (feature group, sample chunk), XCD aware: workgroup ids are
-// dealt to the XCDs round-robin, so chunks are dealt the same way and all
-// feature groups of one chunk run back to back on one XCD, where they share
-// that XCD's L2 lines of x, of the bin indices and of dx.
+// Workgroup -> (feature group g, sample chunk c), XCD aware.  Workgroup ids
+// are dealt to the XCDs round-robin; tiles are numbered chunk-major
+// (t = c * G + g) and each XCD takes one contiguous run of tiles.  The feature
+// groups of a chunk, which share that chunk's cache lines of x, of the bin
+// indices and of dx, therefore run on one XCD and share its L2; with fewer
+// chunks than XCDs a chunk's feature range is split between XCDs instead of
+// piling onto one.  The grid is kNumXcd * tiles_per_xcd(G, C) workgroups.
+__host__ __device__ __forceinline__ int64_t tiles_per_xcd(int64_t G, int64_t C) {
+    return (G * C + kNumXcd - 1) / kNumXcd;
+}
+
 __device__ __forceinline__ bool decode_tile(int bid, int G, int C, int &g, int &c) {
     const int x8 = bid % kNumXcd;
-    const int L = bid / kNumXcd;
-    g = L % G;
-    c = (L / G) * kNumXcd + x8;
-    return c < C;
+    const int64_t L = bid / kNumXcd;
+    const int64_t tpx = tiles_per_xcd(G, C);
+    const int64_t t = x8 * tpx + L;
+    if (L >= tpx || t >= static_cast<int64_t>(G) * C) return false;
+    c = static_cast<int>(t / G);
+    g = static_cast<int>(t - static_cast<int64_t>(c) * G);
+    return true;
 }
 
 }  // namespace ple

@@ -34,7 +34,7 @@ struct FwdArgs {
     int F, B, D;
     int FS;       // features per workgroup (power of two, FS * D/VEC <= 64)
     int G;        // feature groups = ceil(F / FS)
-    int C;        // sample chunks (multiple of kNumXcd)
+    int C;        // sample chunks
     int64_t NC;   // samples per chunk
 };
 
@@ -250,7 +250,7 @@ struct FwdPlan {
 
 // FS: the widest power-of-two feature group whose row fits one wave's stores
 // (FS * D/VEC <= 64) and whose tables fit kLdsBudget.  Chunks: about 32
-// workgroups per CU over the grid, a multiple of the XCD count.
+// workgroups per CU over the grid.
 // PLE_FWD_FS / PLE_FWD_WG_PER_CU override the two choices (tuning).
 bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, bool aligned16, FwdPlan &pl) {
     pl.vec = (D % 4 == 0 && aligned16) ? 4 : 1;
@@ -273,10 +273,8 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, bool aligned16, Fw
     const int64_t max_c = (N + sw - 1) / sw;          // at least one wave tile per chunk
     if (c > max_c) c = max_c;
     if (c < 1) c = 1;
-    c = ((c + kNumXcd - 1) / kNumXcd) * kNumXcd;
     pl.NC = (N + c - 1) / c;
     pl.C = static_cast<int>((N + pl.NC - 1) / pl.NC);
-    pl.C = ((pl.C + kNumXcd - 1) / kNumXcd) * kNumXcd;
     return true;
 }
 
@@ -317,7 +315,7 @@ int forward_run(const ForwardRequest &r) {
     a.bias = r.bias; a.out = r.out; a.idx = r.idx;
     a.N = r.N; a.F = static_cast<int>(r.F); a.B = static_cast<int>(r.B); a.D = static_cast<int>(r.D);
     a.FS = pl.FS; a.G = pl.G; a.C = pl.C; a.NC = pl.NC;
-    const int64_t grid = static_cast<int64_t>(pl.G) * pl.C;
+    const int64_t grid = kNumXcd * tiles_per_xcd(pl.G, pl.C);
     if (grid > INT32_MAX) return PLE_E_TOO_LARGE;
     const int idxb = idx_bytes_for(r.B);
     hipError_t e;

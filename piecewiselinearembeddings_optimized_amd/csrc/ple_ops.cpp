@@ -231,7 +231,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> run_backward(
                                              : at::empty({0}, weight.options());
     if (N == 0 || (!compute_grad_x && !compute_grad_weight && !compute_grad_bias))
         return {grad_x, grad_weight, grad_bias};
-    const size_t ws_bytes = (compute_grad_weight || compute_grad_bias) ? ple_backward_workspace_bytes(N, F, B, D) : 0;
+    const size_t ws_bytes = ple_backward_workspace_bytes(N, F, B, D);
     at::Tensor workspace = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)}, x.options().dtype(at::kByte));
     const int rc = ple_backward_launch(
         grad_output.data_ptr(), x.data_ptr<float>(), bin_edges.data_ptr<float>(),

@@ -82,6 +82,21 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     assert lib.ple_backward_launch(*[None] * 7, dummy, None, None, 4, 2, 3, 2, 0, 0, None, 0, None) == -1
 
 
+def test_ctypes_binding_declares_the_header_and_maps_errors():
+    from piecewiselinearembeddings_optimized_amd import capi
+
+    L = capi.lib()
+    for n in _header_functions():
+        assert getattr(L, n).argtypes is not None, n
+    capi.check(0)
+    with pytest.raises(capi.PleError, match="combination not supported") as ei:
+        capi.check(-7)
+    assert ei.value.code == -7
+    assert capi.workspace_bytes(0, 2, 3, 4) == 0
+    assert capi.workspace_bytes(1024, 8, 48, 24) > 0
+    assert capi.workspace_bytes(1024, 8, 48, 65) == 0      # rejected sizes need nothing
+
+
 def test_operator_schemas_match_reference():
     ops = torch.ops.rtdl_num_embeddings_cuda
     for name, schema in REFERENCE_SCHEMAS.items():
