@@ -6,8 +6,12 @@ backward (dx, dW, db) of the fused operators over one batch of the headline
 workload (configs[1]: N=65536, F=128, 48 bins, d=32, fp32), inputs resident in
 HBM before the timed region starts.  Prints ONE JSON line.
 
-    python bench.py [--steps K] [--warmup W] [--config 1] [--mode fwdbwd|fwd]
+    python bench.py [--steps K] [--warmup W] [--config 1] [--mode fwdbwd|fwd|copy]
                     [--no-cpu-baseline]
+
+``--mode copy`` times a plain 1 GiB device-to-device copy instead (the
+reference kernel for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters to
+bytes).
 
 Timing follows the reference harness's discipline (warm-up, then timed
 repetitions between device events on the stream the kernels run on).  The
@@ -35,7 +39,7 @@ def _parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=1)
-    ap.add_argument("--mode", choices=("fwdbwd", "fwd"), default="fwdbwd")
+    ap.add_argument("--mode", choices=("fwdbwd", "fwd", "copy"), default="fwdbwd")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=4096, help="rows of the workload timed on the CPU")
     return ap.parse_args()
@@ -81,8 +85,34 @@ def _cpu_baseline(w, n_rows: int):
     }
 
 
+def _copy_calibration(args):
+    """1 GiB copy: what FETCH_SIZE / WRITE_SIZE read for known traffic."""
+    import torch
+
+    n = 256 * 1024 * 1024
+    src = torch.ones(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(max(args.warmup, 1)):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    print(json.dumps({"metric": "device copy GB/s (read + write)", "value": 2 * n * 4 / (ms * 1e-3) / 1e9,
+                      "unit": "GB/s", "bytes_read_per_copy": n * 4, "bytes_written_per_copy": n * 4,
+                      "ms_per_copy": ms, "steps": args.steps}), flush=True)
+
+
 def main():
     args = _parse()
+    if args.mode == "copy":
+        _copy_calibration(args)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} (WORLD_SIZE={world}) is not supported: "

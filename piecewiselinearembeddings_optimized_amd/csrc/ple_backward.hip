@@ -22,14 +22,18 @@
 //   sub-tiles; nothing but the gradient stream and LDS work.  Lane groups
 //   (D/VEC lanes, one grad_output row per step) take equal runs of pieces:
 //   each row is read once, its dx is the lane group's DPP-reduced dot with
-//   the LDS weight row (written straight to dx), and bucket / weighted / bias
-//   sums run in registers until the key changes (checked once per piece).
-//   A run's first key goes to a per-run record, every later key straight into
-//   the LDS histogram (no other run can own it); the records are added run
-//   by run in order.  The next sub-tile's descriptors travel while the
-//   current one is reduced.  The chunk's histogram is written once;
-//   ple_bwd_finalize_kernel sums the chunks in chunk order and takes the
-//   suffix over bins.
+//   the LDS weight row (kept in LDS at its sorted position), and bucket /
+//   weighted / bias sums run in registers until the key changes (checked
+//   once per piece).  A run's first key goes to a per-run record, every
+//   later key straight into the LDS histogram (no other run can own it); the
+//   records are added run by run in order.  The sub-tile's dx leaves
+//   feature-major through an inverse permutation (whole-line stores).  The
+//   next sub-tile's descriptors travel while the current one is reduced.
+//   The chunk's histogram is written once.
+//
+// ple_bwd_dx_transpose_kernel turns the feature-major dx into [N, F];
+// ple_bwd_finalize_kernel sums the chunks in chunk order and takes the
+// suffix over bins.
 //
 // No floating-point atomics anywhere, a fixed order for every sum, so results
 // repeat bitwise.
