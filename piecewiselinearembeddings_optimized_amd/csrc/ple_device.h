@@ -31,11 +31,17 @@ __device__ __forceinline__ uint16_t bf16_bits(float v) {
     return static_cast<uint16_t>(__float_as_uint(bf16_round(v)) >> 16);
 }
 
+// float -> IEEE half (nearest-even).  The empty asm pins v as an fp32 value:
+// without it the compiler may fuse the multiply or fma that produced v with
+// the conversion (v_fma_mix*_f16), rounding once to half instead of first to
+// fp32 and then to half as the reference arithmetic does.
 __device__ __forceinline__ float f16_round(float v) {
+    __asm__ volatile("" : "+v"(v));
     return static_cast<float>(static_cast<_Float16>(v));
 }
 
 __device__ __forceinline__ uint16_t f16_bits(float v) {
+    __asm__ volatile("" : "+v"(v));
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
 }
 

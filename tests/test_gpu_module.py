@@ -97,13 +97,13 @@ def _check_linear0_grads(gpu, x, g, rtol, atol):
         assert bool((err <= atol + rtol * s).all()), float((err / (atol + rtol * s)).max())
 
 
-def _amp_reference(cpu, x):
-    """The reference module under bf16 autocast, evaluated on the CPU: PLE
-    branch rounded through bf16 (encoding and weights), fp32 accumulation,
-    bf16 result, then the fp32 bias / residual."""
+def _amp_reference(cpu, x, dtype=torch.bfloat16):
+    """The reference module under ``dtype`` autocast, evaluated on the CPU: PLE
+    branch rounded through ``dtype`` (encoding and weights), fp32
+    accumulation, ``dtype`` result, then the fp32 bias / residual."""
     enc = cpu.impl(x)
-    x_ple = (enc.to(torch.bfloat16).float().transpose(0, 1) @ cpu.linear.weight.to(torch.bfloat16).float())
-    x_ple = x_ple.transpose(0, 1).to(torch.bfloat16)
+    x_ple = (enc.to(dtype).float().transpose(0, 1) @ cpu.linear.weight.to(dtype).float())
+    x_ple = x_ple.transpose(0, 1).to(dtype)
     out = x_ple.float() + cpu.linear.bias if cpu.linear.bias is not None else x_ple
     if cpu.activation is not None:
         out = cpu.activation(out)
@@ -112,25 +112,31 @@ def _amp_reference(cpu, x):
     return out
 
 
+AMP_DTYPES = pytest.mark.parametrize("amp_dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+
+
+@AMP_DTYPES
 @GRID
-def test_forward_amp_bfloat16_matches(case_name, version, activation, seed, d):
+def test_forward_amp_matches(case_name, version, activation, seed, d, amp_dtype):
     bins, cpu, gpu = _modules(case_name, d, activation, version, seed)
     x = sample_features(bins, batch_size=128, seed=seed + 4000)
     with torch.no_grad():
-        expected = _amp_reference(cpu, x)
-        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        expected = _amp_reference(cpu, x, amp_dtype)
+        with torch.autocast(device_type="cuda", dtype=amp_dtype):
             actual = gpu(x.cuda())
+    assert actual.dtype == expected.dtype
     torch.testing.assert_close(actual.float().cpu(), expected.float(), rtol=AMP_FORWARD_RTOL, atol=AMP_FORWARD_ATOL)
 
 
+@AMP_DTYPES
 @GRID
-def test_backward_amp_bfloat16_matches(case_name, version, activation, seed, d):
+def test_backward_amp_matches(case_name, version, activation, seed, d, amp_dtype):
     bins, cpu, gpu = _modules(case_name, d, activation, version, seed)
     xb = sample_features(bins, batch_size=128, seed=seed + 5000)
     xc = xb.clone().requires_grad_(True)
     xg = xb.cuda().requires_grad_(True)
-    oc = _amp_reference(cpu, xc)
-    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+    oc = _amp_reference(cpu, xc, amp_dtype)
+    with torch.autocast(device_type="cuda", dtype=amp_dtype):
         og = gpu(xg)
     torch.manual_seed(seed + 6000)
     g = torch.randn(oc.shape, dtype=torch.float32).to(oc.dtype)

@@ -85,6 +85,43 @@ def test_forward_matches_oracle(cfg, c_oracle):
         assert rel <= BF16_RTOL
 
 
+@pytest.mark.parametrize("cfg", [0, 1, 2])
+def test_forward_float16_matches_oracle(cfg, c_oracle):
+    """fp16 output (the autocast-fp16 path): the fraction, the weights and the
+    result round through IEEE half; bit-exact against the C mirror."""
+    w = workloads.make(cfg, REDUCED[cfg])
+    print(f"forward f16 {w.name} shape={w.shape}", flush=True)
+    x, e, iw, nb, wt, bt = _inputs(w)
+    out, idx = ops.forward(x, e, iw, nb, wt, torch.float16)
+    assert out.dtype == torch.float16
+    np.testing.assert_array_equal(idx.cpu().numpy().astype(np.int64), po.bin_indices(w.x, w.edges, w.n_bins))
+    mirror, _ = c_oracle.forward_f32(w.x, w.edges, w.inv_widths, w.n_bins, w.weight, quant="f16")
+    got = out.float().cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), mirror.view(np.uint32))
+    ref, _, s = po.forward(w.x, w.edges, w.inv_widths, w.n_bins, w.weight, quant="f16", return_abs=True)
+    # half's subnormal quantum (2^-24) bounds the rounding error near zero
+    _report("out vs fp64 (f16 rounding, bf16 bar)", *close_scaled(got, ref, s, BF16_RTOL, 2.0 ** -24))
+    ref32, _ = po.forward(w.x, w.edges, w.inv_widths, w.n_bins, w.weight, quant="f32")
+    rel = normwise_rel(got, ref32)
+    print(f"  out vs unrounded fp64: normwise relative error {rel:.3g}", flush=True)
+    assert rel <= 1e-3   # half keeps 11 significant bits
+
+
+@pytest.mark.parametrize("cfg", [0, 1, 2])
+def test_backward_float16_grad_matches_oracle(cfg, c_oracle):
+    """fp16 gradient with fp16 quantisation (the backward of the autocast-fp16
+    forward): dx / dW against the fp16-aware float64 oracle at the fp32 bar."""
+    w = workloads.make(cfg, REDUCED[cfg])
+    n, f, bmax, d = w.shape
+    print(f"backward f16 {w.name} shape={w.shape}", flush=True)
+    x, e, iw, nb, wt, bt = _inputs(w)
+    _, idx = ops.forward(x, e, iw, nb, wt, torch.float16)
+    g_h = torch.from_numpy(_grad((n, f, d), 300 + cfg)).to(torch.float16)
+    gx, gw = ops.backward(g_h.to(DEV), x, e, iw, nb, wt, idx, True, True)
+    torch.cuda.synchronize()
+    _check_backward(w, "f16", g_h.float().numpy(), gx, gw, None, c_oracle)
+
+
 @pytest.mark.parametrize("cfg", [0, 1, 2, 3])
 def test_forward_with_bias_matches_oracle(cfg, c_oracle):
     w = workloads.make(cfg, REDUCED[cfg])
