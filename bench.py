@@ -6,12 +6,15 @@ backward (dx, dW, db) of the fused operators over one batch of the headline
 workload (configs[1]: N=65536, F=128, 48 bins, d=32, fp32), inputs resident in
 HBM before the timed region starts.  Prints ONE JSON line.
 
-    python bench.py [--steps K] [--warmup W] [--config 1] [--mode fwdbwd|fwd|copy]
+    python bench.py [--steps K] [--warmup W] [--config 1] [--mode fwdbwd|fwd|module|copy]
                     [--no-cpu-baseline]
 
 ``--mode copy`` times a plain 1 GiB device-to-device copy instead (the
 reference kernel for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters to
-bytes).
+bytes).  ``--mode module`` times the whole module in the reference
+benchmark's configuration (version B, no activation; forward and
+forward+backward), fused against the reference's op sequence (the forward
+operator followed by PyTorch's linear0 and residual add).
 
 Timing follows the reference harness's discipline (warm-up, then timed
 repetitions between device events on the stream the kernels run on).  The
@@ -39,7 +42,9 @@ def _parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=1)
-    ap.add_argument("--mode", choices=("fwdbwd", "fwd", "copy"), default="fwdbwd")
+    ap.add_argument("--mode", choices=("fwdbwd", "fwd", "module", "copy"), default="fwdbwd")
+    ap.add_argument("--version", choices=("A", "B"), default="B", help="module version (--mode module)")
+    ap.add_argument("--activation", action="store_true", help="ReLU in the module (--mode module)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=4096, help="rows of the workload timed on the CPU")
     return ap.parse_args()
@@ -108,10 +113,79 @@ def _copy_calibration(args):
                       "ms_per_copy": ms, "steps": args.steps}), flush=True)
 
 
+def _module_bench(args):
+    """Module fwd and fwd+bwd: fused tail vs the reference's op sequence."""
+    import torch
+
+    import rtdl_num_embeddings_cuda
+    from piecewiselinearembeddings_optimized_amd import workloads
+
+    dev = torch.device("cuda:0")
+    w = workloads.make(args.config)
+    n, f, bmax, d = w.shape
+    bins = [torch.from_numpy(w.edges[i, : int(w.n_bins[i]) + 1].copy()) for i in range(f)]
+    torch.manual_seed(0)
+    m = rtdl_num_embeddings_cuda.CudaPiecewiseLinearEmbeddings(bins, d, activation=args.activation,
+                                                                version=args.version).to(dev)
+    torch.nn.init.uniform_(m.linear.weight, -0.2, 0.2)
+    ops = torch.ops.rtdl_num_embeddings_cuda
+    x = torch.from_numpy(w.x).to(dev).requires_grad_(True)
+    g = torch.randn((n, f, d), device=dev, generator=torch.Generator(dev).manual_seed(0))
+
+    def unfused(xx):
+        x_ple, _ = ops.forward(xx, m._cuda_bin_edges, m._cuda_inv_bin_widths, m._cuda_n_bins, m.linear.weight,
+                               torch.float32)
+        if m.linear.bias is not None:
+            x_ple = x_ple + m.linear.bias
+        if m.activation is not None:
+            x_ple = m.activation(x_ple)
+        return x_ple if m.linear0 is None else m.linear0(xx) + x_ple
+
+    def timed(fn, backward):
+        def step():
+            out = fn(x)
+            if backward:
+                out.backward(g)
+        for _ in range(max(args.warmup, 1)):
+            step()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(args.steps):
+            step()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / args.steps
+
+    res = {}
+    for name, fn in (("fused", m), ("reference_ops", unfused)):
+        with torch.no_grad():
+            res[f"{name}_fwd_ms"] = timed(fn, False)
+        res[f"{name}_fwdbwd_ms"] = timed(fn, True)
+    line = {
+        "metric": f"module fwd+bwd samples/s (version {args.version}, activation={args.activation}, {w.name})",
+        "value": n / (res["fused_fwdbwd_ms"] * 1e-3),
+        "unit": "samples/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": res["fused_fwdbwd_ms"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": w.name, "N": n, "F": f, "bins": bmax, "d": d, "version": args.version,
+                   "activation": args.activation, "mode": "module"},
+        **res,
+        "speedup_fwd": res["reference_ops_fwd_ms"] / res["fused_fwd_ms"],
+        "speedup_fwdbwd": res["reference_ops_fwdbwd_ms"] / res["fused_fwdbwd_ms"],
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = _parse()
     if args.mode == "copy":
         _copy_calibration(args)
+        return
+    if args.mode == "module":
+        _module_bench(args)
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -15,6 +15,10 @@
  *                           (registered at csrc/ops.cpp:35-44, :62-75)
  *   ple_backward_launch  <- ple_backward_cuda  csrc/backward_cuda.cu:1528-1725
  *                           (registered at csrc/ops.cpp:46-58, :62-75)
+ *   ple_forward_epilogue_launch / ple_backward_epilogue_launch
+ *                        <- the module tail run as PyTorch ops after the
+ *                           forward operator, src/rtdl_num_embeddings_cuda/
+ *                           module.py:230-248 (no operator counterpart)
  * The reference exposes these only through the torch dispatcher; this ABI is
  * the layer under this build's own dispatcher registration, and is what a
  * ctypes / cgo / JNI binding would call.
@@ -113,6 +117,55 @@ int ple_backward_launch(const void *grad_output, const float *x, const float *bi
                         float *grad_weight, float *grad_bias, int64_t N, int64_t F,
                         int64_t B, int64_t D, int grad_dtype, int quant_dtype,
                         void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Module epilogue fused into the kernels.  No counterpart in the reference's
+ * operator API: the reference module runs this tail as separate PyTorch ops
+ * after its forward operator (src/rtdl_num_embeddings_cuda/module.py:230-248).
+ *   version A:  v = x_ple + bias;             out = relu ? relu(v) : v
+ *   version B:  out = (lin_bias + lin_weight * x) + (relu ? relu(x_ple) : x_ple)
+ * where x_ple is ple_forward_launch's output (rounded through quant_dtype) and
+ * the arithmetic after it is fp32 (the output is float32).  relu follows
+ * torch.relu: NaN passes, v <= 0 gives 0.  With relu, relu_mask holds one bit
+ * per element, bit (j % 32) of word [n, f, j / 32] set where the ReLU passed
+ * its input; the forward writes it (when non-NULL) and the backward reads it.
+ */
+typedef struct ple_epilogue {
+    const float *bias;          /* [F, D] or NULL (version A) */
+    const float *lin_weight;    /* [F, D] or NULL: linear0 weight (version B) */
+    const float *lin_bias;      /* [F, D] linear0 bias, required with lin_weight */
+    int relu;                   /* 0 or 1 */
+    uint32_t *relu_mask;        /* [N, F, ceil(D / 32)] uint32, see above */
+} ple_epilogue_t;
+
+/* Forward with an epilogue: exactly one of bias / lin_weight non-NULL;
+ * output float32 [N, F, D]; other arguments as ple_forward_launch. */
+int ple_forward_epilogue_launch(const float *x, const float *bin_edges, const float *inv_bin_widths,
+                                const int32_t *n_bins, const float *weight,
+                                const ple_epilogue_t *epilogue, float *output, void *bin_indices,
+                                int64_t N, int64_t F, int64_t B, int64_t D, int quant_dtype,
+                                void *stream);
+
+/*
+ * Backward of ple_forward_epilogue_launch (grad_output float32 [N, F, D]).
+ * With g_ple = relu ? grad_output * pass : grad_output, rounded through
+ * quant_dtype for grad_x / grad_weight as in ple_backward_launch, and
+ * grad_x += <grad_output[n, f], lin_weight[f]> for version B;
+ *   grad_bias[f]       = sum_n g_ple (unrounded)         (version A)
+ *   grad_lin_weight[f] = sum_n grad_output[n, f] * x[n, f] (version B)
+ *   grad_lin_bias[f]   = sum_n grad_output[n, f]           (version B)
+ * The backward reads lin_weight (non-NULL: version B, else version A), relu
+ * and relu_mask; bias and lin_bias are not read.  Any gradient pointer may be
+ * NULL; grad_bias must be NULL for version B and the linear0 gradients NULL
+ * for version A.  The workspace is sized by ple_backward_workspace_bytes.
+ */
+int ple_backward_epilogue_launch(const float *grad_output, const float *x, const float *bin_edges,
+                                 const float *inv_bin_widths, const int32_t *n_bins,
+                                 const float *weight, const void *bin_indices,
+                                 const ple_epilogue_t *epilogue, float *grad_x, float *grad_weight,
+                                 float *grad_bias, float *grad_lin_weight, float *grad_lin_bias,
+                                 int64_t N, int64_t F, int64_t B, int64_t D, int quant_dtype,
+                                 void *workspace, size_t workspace_bytes, void *stream);
 
 /* Human-readable name of a return code (static storage). */
 const char *ple_error_string(int code);

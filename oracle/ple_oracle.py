@@ -406,3 +406,55 @@ def module_forward(x, bins_tables, weight, bias=None, linear0=None, activation=F
         x64 = np.asarray(x, dtype=np.float32).astype(np.float64)
         out = out + (np.asarray(b0, np.float64)[None] + np.asarray(w0, np.float64)[None] * x64[..., None])
     return out, idx, pre
+
+
+def relu_pass(pre: np.ndarray) -> np.ndarray:
+    """Where torch.relu passes its input's gradient: ``not (v <= 0)`` (NaN passes)."""
+    with np.errstate(invalid="ignore"):
+        return ~(np.asarray(pre) <= 0)
+
+
+def pack_pass_bits(passm: np.ndarray) -> np.ndarray:
+    """[N, F, D] bool -> int32 [N, F, ceil(D / 32)]: bit j % 32 of word j // 32."""
+    n, f, d = passm.shape
+    words = (d + 31) // 32
+    out = np.zeros((n, f, words), dtype=np.uint32)
+    for j in range(d):
+        out[:, :, j // 32] |= passm[:, :, j].astype(np.uint32) << np.uint32(j % 32)
+    return out.view(np.int32)
+
+
+def unpack_pass_bits(words: np.ndarray, d: int) -> np.ndarray:
+    w = np.asarray(words).view(np.uint32)
+    return np.stack([((w[:, :, j // 32] >> np.uint32(j % 32)) & 1).astype(bool) for j in range(d)], axis=-1)
+
+
+def module_backward(grad_output, x, bins_tables, weight, idx, pass_mask=None, has_bias=True, linear0=None,
+                    quant="f32"):
+    """Gradients of :func:`module_forward` in float64 (``module.py:230-248``).
+
+    ``g_v = g * pass`` behind a ReLU; the PLE branch sees ``q(g_v)`` (fp32 then
+    ``quant``, as autograd casts the gradient to ``x_ple``'s dtype) and
+    :func:`backward` gives dx / dW; version A's bias gradient is ``sum_n g_v``;
+    version B adds ``dx += <g, w0>``, ``d w0 = sum_n g x``, ``d b0 = sum_n g``.
+    Every result has an ``*_abs`` companion (sum of |terms|).
+    """
+    edges, iw, n_bins = bins_tables
+    g = np.asarray(grad_output, dtype=np.float64)
+    gv = g if pass_mask is None else np.where(pass_mask, g, 0.0)
+    gq = quantize(gv.astype(np.float32), quant)
+    r = backward(gq, x, edges, iw, n_bins, weight, idx, quant=quant, grad_bias_source=gv)
+    if linear0 is None:
+        if not has_bias:
+            del r["db"], r["db_abs"]
+        return r
+    del r["db"], r["db_abs"]
+    w0, _b0 = linear0
+    x64 = np.asarray(x, dtype=np.float32).astype(np.float64)
+    t = g * np.asarray(w0, dtype=np.float64)[None]
+    r["dx"] = r["dx"] + t.sum(-1)
+    r["dx_abs"] = r["dx_abs"] + np.abs(t).sum(-1)
+    gx = g * x64[..., None]
+    r["dlw"], r["dlw_abs"] = gx.sum(0), np.abs(gx).sum(0)
+    r["dlb"], r["dlb_abs"] = g.sum(0), np.abs(g).sum(0)
+    return r

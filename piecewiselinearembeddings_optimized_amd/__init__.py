@@ -4,7 +4,8 @@ Drop-in for the reference package ``rtdl_num_embeddings_cuda`` (also
 importable under that name): the same ``torch.ops.rtdl_num_embeddings_cuda``
 operators, FakeTensor and autograd registrations, and the
 ``CudaPiecewiseLinearEmbeddings`` module, running hand-written HIP kernels for
-gfx950 (``csrc/ple_kernels.hip``) behind the C ABI of ``include/ple_hip.h``.
+gfx950 (``csrc/ple_forward.hip``, ``csrc/ple_backward.hip``) behind the C ABI
+of ``include/ple_hip.h`` (``csrc/ple_capi.hip``).
 
 Import order follows the reference (``__init__.py:3-7`` there): the native
 registrations first, then the fake kernels, then autograd, then the module.

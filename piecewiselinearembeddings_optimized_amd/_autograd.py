@@ -8,7 +8,13 @@ returns gradients for ``x`` (input 0) and ``weight`` (input 4) only.
 ``forward_with_bias``: additionally returns the bias gradient (input 5) from
 the same backward launch; ``quant_dtype`` (input 6) is forwarded so the
 backward rounds the gradient, the fraction and the weights like the forward
-did.  Double backward is not implemented (as in the reference).
+did.
+
+``forward_epilogue``: gradients for ``x`` (0), ``weight`` (4), ``bias`` (5),
+``lin_weight`` (6) and ``lin_bias`` (7) from one backward launch, which reads
+the forward's ReLU pass bits (saved, non-differentiable).
+
+Double backward is not implemented (as in the reference).
 """
 
 from __future__ import annotations
@@ -82,4 +88,38 @@ torch.library.register_autograd(
     "rtdl_num_embeddings_cuda::forward_with_bias",
     _forward_with_bias_backward,
     setup_context=_setup_forward_with_bias_context,
+)
+
+
+def _setup_forward_epilogue_context(ctx: Any, inputs, output) -> None:
+    x, bin_edges, inv_bin_widths, n_bins, weight, _bias, lin_weight, _lin_bias, relu, _save, quant_dtype = inputs
+    _out, bin_indices, relu_mask = output
+    ctx.save_for_backward(x, bin_edges, inv_bin_widths, n_bins, weight, bin_indices, relu_mask, lin_weight)
+    ctx.relu = bool(relu)
+    ctx.quant_dtype = quant_dtype
+    ctx.mark_non_differentiable(bin_indices, relu_mask)
+    ctx.set_materialize_grads(False)
+
+
+def _forward_epilogue_backward(ctx: Any, grad_output, _grad_bin_indices, _grad_relu_mask):
+    if grad_output is None:
+        return (None,) * 11
+    x, bin_edges, inv_bin_widths, n_bins, weight, bin_indices, relu_mask, lin_weight = ctx.saved_tensors
+    need = [bool(ctx.needs_input_grad[i]) for i in (0, 4, 5, 6, 7)]
+    if ctx.relu and relu_mask.numel() == 0:
+        raise RuntimeError("forward_epilogue was called with save_mask=False; its ReLU cannot be differentiated")
+    gx, gw, gb, glw, glb = _ops.backward_epilogue(
+        grad_output.contiguous(), x, bin_edges, inv_bin_widths, n_bins, weight, bin_indices, relu_mask,
+        lin_weight, ctx.relu, ctx.quant_dtype, *need,
+    )
+    return (
+        gx if need[0] else None, None, None, None, gw if need[1] else None, gb if need[2] else None,
+        glw if need[3] else None, glb if need[4] else None, None, None, None,
+    )
+
+
+torch.library.register_autograd(
+    "rtdl_num_embeddings_cuda::forward_epilogue",
+    _forward_epilogue_backward,
+    setup_context=_setup_forward_epilogue_context,
 )

@@ -3,8 +3,8 @@
 They state the shape / dtype contract of every operator without touching
 data, so ``torch.compile(fullgraph=True)`` and meta-device tracing work.  The
 checks and messages of ``forward`` / ``backward`` follow the reference
-(``src/rtdl_num_embeddings_cuda/_meta.py:22-188``); the ``*_with_bias``
-operators are this build's fused variants.
+(``src/rtdl_num_embeddings_cuda/_meta.py:22-188``); the ``*_with_bias`` and
+``*_epilogue`` operators are this build's fused variants.
 """
 
 from __future__ import annotations
@@ -101,3 +101,60 @@ def _backward_with_bias_fake(grad_output, x, bin_edges, inv_bin_widths, n_bins, 
         else torch.empty((0,), dtype=weight.dtype, device=weight.device)
     )
     return _maybe(x, x, compute_grad_x), _maybe(weight, weight, compute_grad_weight), grad_bias
+
+
+def _check_fd(t, weight, name: str) -> None:
+    torch._check(t.ndim == 2, lambda: f"{name} must have shape [F, D]")
+    torch._check(t.shape[0] == weight.shape[0], lambda: f"{name} must have shape [F, D]")
+    torch._check(t.shape[1] == weight.shape[2], lambda: f"{name} must have shape [F, D]")
+    torch._check(t.dtype == torch.float32, lambda: f"{name} must be float32")
+
+
+def _mask_words(d_embedding) -> int:
+    return (d_embedding + 31) // 32
+
+
+@torch.library.register_fake("rtdl_num_embeddings_cuda::forward_epilogue")
+def _forward_epilogue_fake(x, bin_edges, inv_bin_widths, n_bins, weight, bias, lin_weight, lin_bias, relu,
+                           save_mask, quant_dtype):
+    _check_forward_inputs(x, bin_edges, inv_bin_widths, n_bins, weight)
+    torch._check(quant_dtype in SUPPORTED_OUTPUT_DTYPES, lambda: "Unsupported quant dtype")
+    torch._check((bias is None) != (lin_weight is None), lambda: "exactly one of bias and lin_weight must be given")
+    if bias is not None:
+        _check_fd(bias, weight, "bias")
+    if lin_weight is not None:
+        torch._check(lin_bias is not None, lambda: "lin_bias must be given with lin_weight")
+        _check_fd(lin_weight, weight, "lin_weight")
+        _check_fd(lin_bias, weight, "lin_bias")
+    out, idx = _forward_outputs(x, weight, torch.float32)
+    if relu and save_mask:
+        mask = torch.empty((x.shape[0], x.shape[1], _mask_words(weight.shape[2])), dtype=torch.int32,
+                           device=x.device)
+    else:
+        mask = torch.empty((0,), dtype=torch.int32, device=x.device)
+    return out, idx, mask
+
+
+@torch.library.register_fake("rtdl_num_embeddings_cuda::backward_epilogue")
+def _backward_epilogue_fake(grad_output, x, bin_edges, inv_bin_widths, n_bins, weight, bin_indices, relu_mask,
+                            lin_weight, relu, quant_dtype, compute_grad_x, compute_grad_weight,
+                            compute_grad_bias, compute_grad_lin_weight, compute_grad_lin_bias):
+    _check_backward_inputs(grad_output, x, weight, bin_indices)
+    torch._check(grad_output.dtype == torch.float32, lambda: "grad_output must be float32")
+    torch._check(quant_dtype in SUPPORTED_OUTPUT_DTYPES, lambda: "Unsupported quant dtype")
+    if lin_weight is not None:
+        _check_fd(lin_weight, weight, "lin_weight")
+    torch._check(not (lin_weight is not None and compute_grad_bias),
+                 lambda: "no bias gradient with lin_weight (version B has no bias)")
+    torch._check(lin_weight is not None or not (compute_grad_lin_weight or compute_grad_lin_bias),
+                 lambda: "linear0 gradients need lin_weight")
+    if relu:
+        torch._check(relu_mask.ndim == 3 and relu_mask.dtype == torch.int32,
+                     lambda: "relu_mask must be the int32 [N, F, ceil(D / 32)] pass bits of the forward")
+
+    def fd(wanted: bool) -> Tensor:
+        shape = (weight.shape[0], weight.shape[2]) if wanted else (0,)
+        return torch.empty(shape, dtype=weight.dtype, device=weight.device)
+
+    return (_maybe(x, x, compute_grad_x), _maybe(weight, weight, compute_grad_weight), fd(compute_grad_bias),
+            fd(compute_grad_lin_weight), fd(compute_grad_lin_bias))

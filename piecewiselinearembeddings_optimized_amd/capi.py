@@ -25,6 +25,18 @@ _DTYPE_CODES = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat
 _lib = None
 
 
+class Epilogue(ctypes.Structure):
+    """``ple_epilogue_t``: the module tail fused into the kernels."""
+
+    _fields_ = [
+        ("bias", ctypes.c_void_p),
+        ("lin_weight", ctypes.c_void_p),
+        ("lin_bias", ctypes.c_void_p),
+        ("relu", ctypes.c_int),
+        ("relu_mask", ctypes.c_void_p),
+    ]
+
+
 class PleError(RuntimeError):
     def __init__(self, code: int, message: str):
         super().__init__(f"{message} (code {code})")
@@ -48,6 +60,12 @@ def lib() -> ctypes.CDLL:
         L.ple_backward_workspace_bytes.restype = sz
         L.ple_backward_launch.argtypes = [p, p, p, p, p, p, p, p, p, p, i64, i64, i64, i64, i32, i32, p, sz, p]
         L.ple_backward_launch.restype = i32
+        ep = ctypes.POINTER(Epilogue)
+        L.ple_forward_epilogue_launch.argtypes = [p, p, p, p, p, ep, p, p, i64, i64, i64, i64, i32, p]
+        L.ple_forward_epilogue_launch.restype = i32
+        L.ple_backward_epilogue_launch.argtypes = [p, p, p, p, p, p, p, ep, p, p, p, p, p, i64, i64, i64, i64, i32,
+                                                   p, sz, p]
+        L.ple_backward_epilogue_launch.restype = i32
         _lib = L
     return _lib
 
@@ -99,3 +117,37 @@ def backward(grad_output, x, bin_edges, inv_bin_widths, n_bins, weight, bin_indi
         _ptr(grad_output), _ptr(x), _ptr(bin_edges), _ptr(inv_bin_widths), _ptr(n_bins), _ptr(weight),
         _ptr(bin_indices), _ptr(grad_x), _ptr(grad_weight), _ptr(grad_bias), n, f, bmax, d,
         dtype_code(grad_output.dtype), dtype_code(quant_dtype), _ptr(workspace), ws_bytes, _stream(stream)))
+
+
+def epilogue(bias=None, lin_weight=None, lin_bias=None, relu=False, relu_mask=None) -> Epilogue:
+    def addr(t):
+        return None if t is None else t.data_ptr()
+
+    return Epilogue(addr(bias), addr(lin_weight), addr(lin_bias), 1 if relu else 0, addr(relu_mask))
+
+
+def forward_epilogue(x, bin_edges, inv_bin_widths, n_bins, weight, epi: Epilogue, output, bin_indices,
+                     quant_dtype, stream=None) -> None:
+    """``ple_forward_epilogue_launch`` (fp32 ``output``)."""
+    n, f = x.shape
+    _, bmax, d = weight.shape
+    check(lib().ple_forward_epilogue_launch(
+        _ptr(x), _ptr(bin_edges), _ptr(inv_bin_widths), _ptr(n_bins), _ptr(weight), ctypes.byref(epi),
+        _ptr(output), _ptr(bin_indices), n, f, bmax, d, dtype_code(quant_dtype), _stream(stream)))
+
+
+def backward_epilogue(grad_output, x, bin_edges, inv_bin_widths, n_bins, weight, bin_indices, epi: Epilogue,
+                      grad_x, grad_weight, grad_bias, grad_lin_weight, grad_lin_bias, quant_dtype,
+                      workspace=None, stream=None) -> None:
+    """``ple_backward_epilogue_launch``; gradients are caller-provided fp32 tensors or None."""
+    n, f = x.shape
+    _, bmax, d = weight.shape
+    need = workspace_bytes(n, f, bmax, d)
+    if workspace is None and need > 0:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib().ple_backward_epilogue_launch(
+        _ptr(grad_output), _ptr(x), _ptr(bin_edges), _ptr(inv_bin_widths), _ptr(n_bins), _ptr(weight),
+        _ptr(bin_indices), ctypes.byref(epi), _ptr(grad_x), _ptr(grad_weight), _ptr(grad_bias),
+        _ptr(grad_lin_weight), _ptr(grad_lin_bias), n, f, bmax, d, dtype_code(quant_dtype), _ptr(workspace),
+        ws_bytes, _stream(stream)))

@@ -6,6 +6,14 @@
 //                                                 reference backward_cuda.cu:170-336,889-923
 // db[f]    = sum_n g                              (autograd of module.py:238-239)
 //
+// Module epilogues (the backward of the fused forward tails, module.py:230-248;
+// the gradient is then fp32):
+//   ReLU      g_ple = g * pass[n, f, j] (the forward's bits); with a bias,
+//             db = sum_n g_ple
+//   linear0   g_ple = g (or g * pass with ReLU); dx += <g, lin_w[f]>,
+//             d lin_w[f] = sum_n g x, d lin_b[f] = sum_n g (in db's slot)
+// dx and dW use g_ple rounded through the quantisation dtype.
+//
 // Main path: two kernels over tiles of P (sample, feature) pairs (NT samples
 // x FS features, "sub-tiles").
 //
@@ -68,6 +76,11 @@ struct BwdArgs {
     uint32_t *piece; // [T][G][PM] pieces {bin | fl << 12 | first row << 16 | (rows - 1) << 28}
     int *npc;        // [T][G] pieces per sub-tile
     float *dxt;      // [F][N] dx, feature-major (transposed into dx at the end)
+    const uint32_t *mask;   // [N][F][MW] ReLU pass bits of the forward (epilogue with ReLU)
+    const float *lin_w;     // [F][D] linear0 weight (version-B epilogue)
+    float *part_lw;         // [Cd][F][D] chunk partials of the linear0 weight gradient
+    float *dlw;             // [F][D] linear0 weight gradient
+    int MW;                 // mask words per (sample, feature) row
     int64_t N;
     int F, B, D;
     int C;           // chunks (fallback: of samples; sorted path: of sub-tiles)
@@ -78,7 +91,8 @@ struct BwdArgs {
     // sorted path
     int FS, G, NT, T, SPC, PM, LGW, nbits;   // T sub-tiles, SPC sub-tiles per chunk, PM piece capacity
     int so_nb, so_edge, so_iw, so_info, so_rank, so_cnt, so_seg, so_tmp, so_desc, so_piece;   // sort LDS
-    int ro_qw, ro_hist, ro_db, ro_iw, ro_nb, ro_desc, ro_piece, ro_npc, ro_rec, ro_rkey, ro_rfl, ro_dx, ro_inv;   // reduce LDS
+    int ro_qw, ro_hist, ro_db, ro_iw, ro_nb, ro_desc, ro_piece, ro_npc, ro_rec, ro_rkey, ro_rfl, ro_dx, ro_inv,
+        ro_lw, ro_dlw;   // reduce LDS
 };
 
 // Exclusive prefix sum of a[0..n) in place, all kBlock threads.
@@ -118,6 +132,10 @@ constexpr int kL = 4;
 // Piece capacity per sub-tile: at most P / kL + (non-empty keys) pieces.
 constexpr int kMaxPieces = kP / kL + kP;
 constexpr int kPieceRegs = (kMaxPieces + kBlock - 1) / kBlock;
+
+// backward epilogue flags (template argument of the reduce kernel)
+constexpr int kBwdRelu = 1;
+constexpr int kBwdLin = 2;
 
 // ---------------------------------------------------------------------------
 // sort
@@ -278,12 +296,14 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_sort_kernel(BwdArgs a) {
 // reduce
 // ---------------------------------------------------------------------------
 
-template <int GD, int Q, int VEC, int LGW_T>
+template <int GD, int Q, int VEC, int LGW_T, int EPI>
 __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
-    // With fp32 rounding the bias gradient is the sum of the bin buckets
-    // (taken at finalize); otherwise it needs its own sum of the unrounded
-    // gradient.
-    constexpr bool kRawDb = Q != PLE_DTYPE_F32;
+    constexpr bool kRelu = (EPI & kBwdRelu) != 0;
+    constexpr bool kLin = (EPI & kBwdLin) != 0;
+    // With fp32 rounding and no linear0 branch the bias gradient is the sum of
+    // the bin buckets (taken at finalize); otherwise it needs its own sum of
+    // the unrounded (for linear0: unmasked) gradient.
+    constexpr bool kRawDb = Q != PLE_DTYPE_F32 || kLin;
     extern __shared__ __align__(16) unsigned char lds[];
     const int FS = a.FS, B = a.B, D = a.D, F = a.F, NT = a.NT;
     float *s_qw = reinterpret_cast<float *>(lds + a.ro_qw);             // [FS][B][D]
@@ -299,6 +319,8 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
     int *s_rfl = reinterpret_cast<int *>(lds + a.ro_rfl);               // [LG]
     float *s_dx = reinterpret_cast<float *>(lds + a.ro_dx);             // [P+1] dx by sorted row (+ a discard slot)
     uint16_t *s_inv = reinterpret_cast<uint16_t *>(lds + a.ro_inv);     // [P] sorted row of each pair
+    float *s_lw = reinterpret_cast<float *>(lds + a.ro_lw);             // [FS][D] linear0 weight
+    float *s_dlw = reinterpret_cast<float *>(lds + a.ro_dlw);           // [FS][D] sum of g x
 
     int g, c;
     if (!decode_tile(blockIdx.x, a.G, a.C, g, c)) return;
@@ -345,6 +367,12 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
     }
     for (int i = tid; i < FS * B * 2 * D; i += kBlock) s_hist[i] = 0.0f;
     for (int i = tid; i < FS * D; i += kBlock) s_db[i] = 0.0f;
+    if constexpr (kLin) {
+        for (int i = tid; i < FS * D; i += kBlock) {
+            s_lw[i] = i / D < nfh ? a.lin_w[static_cast<int64_t>(f0) * D + i] : 0.0f;
+            s_dlw[i] = 0.0f;
+        }
+    }
     __syncthreads();
     for (int i = tid; i < FS * B * D; i += kBlock) {
         const int fl = i / (B * D);
@@ -364,8 +392,10 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
     const int lg = tid / lgw;
     const int lc = tid - lg * lgw;
     const bool c_ok = lc < D / VEC;
+    const int lcx = c_ok ? lc : 0;               // idle lanes read column 0 (their g is 0)
     const int D2 = 2 * D;
-    const int RS = kRawDb ? 3 * D : 2 * D;        // record stride {bucket | weighted (| raw g)}
+    // record stride {bucket | weighted (| raw g) (| g x)}
+    const int RS = (kRawDb ? 3 * D : 2 * D) + (kLin ? D : 0);
     const int nt_shift = __ffs(NT) - 1;           // NT is a power of two
 
     for (int t = t_begin; t < t_end; ++t) {
@@ -402,9 +432,9 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
             // nothing and need no masking.
             int cur = -1, db_fl = -1;
             bool first_key = true, first_fl = true;
-            float ab[VEC], aw[VEC], ad[VEC];
+            float ab[VEC], aw[VEC], ad[VEC], ax[VEC];
 #pragma unroll
-            for (int q = 0; q < VEC; ++q) ab[q] = aw[q] = ad[q] = 0.0f;
+            for (int q = 0; q < VEC; ++q) ab[q] = aw[q] = ad[q] = ax[q] = 0.0f;
             if (lc == 0) {
                 s_rkey[lg] = -1;
                 s_rfl[lg] = -1;
@@ -442,6 +472,13 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
 #pragma unroll
                     for (int q = 0; q < VEC; ++q) o[q] = first_fl ? ad[q] : o[q] + ad[q];
                     lds_store_vec<VEC>(dst, o);
+                    if constexpr (kLin) {
+                        float *dx2 = first_fl ? rec + D2 + D : s_dlw + db_fl * D + lc * VEC;
+                        lds_load_vec<VEC>(dx2, o);
+#pragma unroll
+                        for (int q = 0; q < VEC; ++q) o[q] = first_fl ? ax[q] : o[q] + ax[q];
+                        lds_store_vec<VEC>(dx2, o);
+                    }
                 }
                 if (first_fl && lc == 0) s_rfl[lg] = db_fl;
                 first_fl = false;
@@ -465,34 +502,61 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
                 static_cast<const char *>(a.g) + (sub * F + f0) * static_cast<int64_t>(D) * esz, span);
             // idle lanes: an offset past every span
             const uint32_t laneoff = c_ok ? static_cast<uint32_t>(lc) * VEC * esz : 0x80000000u;
+            // epilogue inputs of a row (sample s, local feature fl): its mask
+            // word (the one holding this lane's columns) and x; rows past a
+            // piece's end (sample NT) read zeros
+            const int MW = a.MW;
+            const int64_t row0 = sub * F + f0;
+            const __amdgpu_buffer_rsrc_t mrs =
+                make_rsrc(kRelu ? static_cast<const void *>(a.mask + row0 * MW) : a.g,
+                          kRelu ? static_cast<uint32_t>(ns) * F * MW * 4 : 0u);
+            const __amdgpu_buffer_rsrc_t xrs =
+                make_rsrc(kLin ? static_cast<const void *>(a.x + row0) : a.g, kLin ? static_cast<uint32_t>(ns) * F * 4 : 0u);
+            const uint32_t rowMb = static_cast<uint32_t>(F) * MW * 4;
+            const uint32_t m_word_off = static_cast<uint32_t>((lcx * VEC) >> 5) * 4;
+            const int m_shift = (lcx * VEC) & 31;
 
             // Piece t of the run: its entry, its rows' descriptors, and loads
             // of their gradient rows.  Past j1 the piece is empty (all rows
             // read zeros).  Every lane loads, with no branch around the load,
             // so each piece has one counted wait.
-            auto issue = [&](int tt, float (&gv)[kL][VEC], uint2 (&dv)[kL], uint32_t &pe) __attribute__((always_inline)) {
+            auto issue = [&](int tt, float (&gv)[kL][VEC], uint2 (&dv)[kL], uint32_t &pe, uint32_t (&mv)[kL],
+                             float (&xv)[kL]) __attribute__((always_inline)) {
                 const int j = j0 + tt;
                 const bool real = j < j1;
                 pe = s_piece[real ? j : 0];
                 const int rs = static_cast<int>((pe >> 16) & 0xfff);
                 const int n = real ? static_cast<int>(pe >> 28) + 1 : 0;
-                const uint32_t flb = __umul24((pe >> 12) & 0xf, Db) + laneoff;
+                const uint32_t flp = (pe >> 12) & 0xf;
+                const uint32_t flb = __umul24(flp, Db) + laneoff;
 #pragma unroll
                 for (int i = 0; i < kL; ++i) dv[i] = s_sdesc[i < n ? rs + i : kP];
-                // (the 24-bit product ignores the feature bits of .y)
+                // (the 24-bit products ignore the feature bits of .y)
 #pragma unroll
                 for (int i = 0; i < kL; ++i) load_grad_buf<GD, VEC>(grs, __umul24(dv[i].y, rowFb) + flb, gv[i]);
+                if constexpr (kRelu) {
+#pragma unroll
+                    for (int i = 0; i < kL; ++i)
+                        mv[i] = __builtin_amdgcn_raw_buffer_load_b32(
+                            mrs, __umul24(dv[i].y, rowMb) + flp * static_cast<uint32_t>(MW) * 4 + m_word_off, 0, 0);
+                }
+                if constexpr (kLin) {
+#pragma unroll
+                    for (int i = 0; i < kL; ++i)
+                        xv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                            xrs, __umul24(dv[i].y, static_cast<uint32_t>(F) * 4) + flp * 4, 0, 0));
+                }
             };
 
             // weight rows k and k-1 and their inverse widths for the current
             // key, reloaded from LDS when the key changes (idle lanes read
             // column 0; their g is 0); row k-1 serves rows with x on e_k
-            const int lcx = c_ok ? lc : 0;
-            float wk[VEC], wp[VEC];
+            float wk[VEC], wp[VEC], lw[VEC];
             float iwk = 0.0f, iwp = 0.0f;
 #pragma unroll
-            for (int q = 0; q < VEC; ++q) wk[q] = wp[q] = 0.0f;
-            auto process = [&](int tt, const float (&gv)[kL][VEC], const uint2 (&dsc)[kL], uint32_t pe) __attribute__((always_inline)) {
+            for (int q = 0; q < VEC; ++q) wk[q] = wp[q] = lw[q] = 0.0f;
+            auto process = [&](int tt, const float (&gv)[kL][VEC], const uint2 (&dsc)[kL], uint32_t pe,
+                               const uint32_t (&mv)[kL], const float (&xv)[kL]) __attribute__((always_inline)) {
                 const bool real = j0 + tt < j1;
                 const int n = real ? static_cast<int>(pe >> 28) + 1 : 0;
                 const int key = real ? static_cast<int>(pe & 0xffff) : cur;
@@ -505,10 +569,11 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
                         if (fl != db_fl) {
                             flush_fl();
 #pragma unroll
-                            for (int q = 0; q < VEC; ++q) ad[q] = 0.0f;
+                            for (int q = 0; q < VEC; ++q) ad[q] = ax[q] = 0.0f;
                             db_fl = fl;
                         }
                     }
+                    if constexpr (kLin) lds_load_vec<VEC>(s_lw + __umul24(fl, D) + lcx * VEC, lw);
                     cur = key;
                     const int k = key & 0xfff;
                     const int kp = k > 0 ? k - 1 : 0;
@@ -522,18 +587,29 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
 #pragma unroll
                 for (int i = 0; i < kL; ++i) {
                     const float qf = __uint_as_float(dsc[i].x);
-                    float gq[VEC];
-                    float dot = 0.0f, dot2 = 0.0f;
+                    float gq[VEC], gm[VEC];
+                    float dot = 0.0f, dot2 = 0.0f, dotl = 0.0f;
 #pragma unroll
                     for (int q = 0; q < VEC; ++q) {
-                        gq[q] = quant<Q>(gv[i][q]);
+                        // ReLU: the forward's pass bit of column lc * VEC + q
+                        gm[q] = gv[i][q];
+                        if constexpr (kRelu)
+                            gm[q] = __uint_as_float(__float_as_uint(gm[q]) &
+                                                    static_cast<uint32_t>(__builtin_amdgcn_sbfe(
+                                                        static_cast<int>(mv[i]), m_shift + q, 1)));
+                        gq[q] = quant<Q>(gm[q]);
                         ab[q] += gq[q];
                         aw[q] = fmaf(qf, gq[q], aw[q]);
-                        if constexpr (kRawDb) ad[q] += gv[i][q];
+                        if constexpr (kRawDb) ad[q] += kLin ? gv[i][q] : gm[q];
+                        if constexpr (kLin) {
+                            ax[q] = fmaf(gv[i][q], xv[i], ax[q]);
+                            dotl = fmaf(gv[i][q], lw[q], dotl);
+                        }
                         dot = fmaf(gq[q], wk[q], dot);
                         dot2 = fmaf(gq[q], wp[q], dot2);
                     }
                     float part = dot * iwk;
+                    if constexpr (kLin) part += dotl;
                     // x on the bin's left edge (k >= 1): the lower bin's term too
                     part = dsc[i].x == 0x80000000u ? fmaf(dot2, iwp, part) : part;
                     if constexpr (LGW_T > 0) part = group_sum<LGW_T>(part);
@@ -550,17 +626,19 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
             float gA[kL][VEC], gB[kL][VEC];
             uint2 dA[kL], dB[kL];
             uint32_t pA = 0, pB = 0;
+            uint32_t mA[kL], mB[kL];     // (epilogue with ReLU)
+            float xA[kL], xB[kL];        // (epilogue with linear0)
             if (m > 0) {
-                issue(0, gA, dA, pA);
+                issue(0, gA, dA, pA, mA, xA);
                 int tt = 0;
 #pragma unroll 1
                 for (; tt + 1 < m; tt += 2) {
-                    issue(tt + 1, gB, dB, pB);
-                    process(tt, gA, dA, pA);
-                    issue(tt + 2, gA, dA, pA);
-                    process(tt + 1, gB, dB, pB);
+                    issue(tt + 1, gB, dB, pB, mB, xB);
+                    process(tt, gA, dA, pA, mA, xA);
+                    issue(tt + 2, gA, dA, pA, mA, xA);
+                    process(tt + 1, gB, dB, pB, mB, xB);
                 }
-                if (tt < m) process(tt, gA, dA, pA);
+                if (tt < m) process(tt, gA, dA, pA, mA, xA);
             }
             flush_key();
             if constexpr (kRawDb) flush_fl();
@@ -602,16 +680,22 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
             }
             const int rfl = kRawDb ? s_rfl[lg] : -1;
             if (rfl >= 0 && (lg == 0 || s_rfl[lg - 1] != rfl)) {
-                float sd[VEC];
+                float sd[VEC], sx[VEC];
 #pragma unroll
-                for (int q = 0; q < VEC; ++q) sd[q] = 0.0f;
+                for (int q = 0; q < VEC; ++q) sd[q] = sx[q] = 0.0f;
                 for (int j = lg; j < LG && s_rfl[j] == rfl; ++j) {
                     const float *rj = s_rec + j * RS + D2 + lc * VEC;
 #pragma unroll
-                    for (int q = 0; q < VEC; ++q) sd[q] += rj[q];
+                    for (int q = 0; q < VEC; ++q) {
+                        sd[q] += rj[q];
+                        if constexpr (kLin) sx[q] += rj[D + q];
+                    }
                 }
 #pragma unroll
-                for (int q = 0; q < VEC; ++q) s_db[rfl * D + lc * VEC + q] += sd[q];
+                for (int q = 0; q < VEC; ++q) {
+                    s_db[rfl * D + lc * VEC + q] += sd[q];
+                    if constexpr (kLin) s_dlw[rfl * D + lc * VEC + q] += sx[q];
+                }
             }
         }
         // (the next iteration's barrier orders these histogram updates before
@@ -632,6 +716,11 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
             float *dstb = a.part_db + (static_cast<int64_t>(c) * F + f0) * D;
             for (int i = tid; i < FS * D; i += kBlock)
                 if (i / D < nfh) dstb[i] = s_db[i];
+        }
+        if constexpr (kLin) {
+            float *dstl = a.part_lw + (static_cast<int64_t>(c) * F + f0) * D;
+            for (int i = tid; i < FS * D; i += kBlock)
+                if (i / D < nfh) dstl[i] = s_dlw[i];
         }
     }
 }
@@ -657,20 +746,26 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_simple_dx_kernel(BwdArgs a) {
         const float v = a.x[p];
         const bool edge = (k > 0) && (v == a.edges[static_cast<int64_t>(f) * (B + 1) + k]);
         const float *wp = a.weight + (static_cast<int64_t>(f) * B + (k > 0 ? k - 1 : 0)) * D;
-        float s = 0.0f, s2 = 0.0f;
+        float s = 0.0f, s2 = 0.0f, sl = 0.0f;
         for (int j = gl; j < D; j += kLanes) {
-            const float gv = quant<Q>(load_grad<GD>(a.g, p * D + j));
+            const float graw = load_grad<GD>(a.g, p * D + j);
+            float gm = graw;
+            if (a.mask && !((a.mask[p * a.MW + (j >> 5)] >> (j & 31)) & 1u)) gm = 0.0f;
+            const float gv = quant<Q>(gm);
             s = fmaf(gv, quant<Q>(w[j]), s);
             if (edge) s2 = fmaf(gv, quant<Q>(wp[j]), s2);
+            if (a.lin_w) sl = fmaf(graw, a.lin_w[static_cast<int64_t>(f) * D + j], sl);
         }
 #pragma unroll
         for (int off = kLanes / 2; off > 0; off >>= 1) {
             s += __shfl_xor(s, off, kLanes);
             s2 += __shfl_xor(s2, off, kLanes);
+            sl += __shfl_xor(sl, off, kLanes);
         }
         if (gl == 0) {
             float r = s * a.iw[static_cast<int64_t>(f) * B + k];
             if (edge) r = fmaf(s2, a.iw[static_cast<int64_t>(f) * B + k - 1], r);
+            if (a.lin_w) r += sl;
             a.dx[p] = r;
         }
     }
@@ -700,12 +795,13 @@ __global__ __launch_bounds__(kWave) void ple_bwd_simple_hist_kernel(BwdArgs a) {
     const float *e = a.edges + static_cast<int64_t>(f) * (B + 1);
     const float *iwr = a.iw + static_cast<int64_t>(f) * B;
     int kc = -1;
-    float cb = 0.0f, cw = 0.0f, cdb = 0.0f;
+    float cb = 0.0f, cw = 0.0f, cdb = 0.0f, clw = 0.0f;
     constexpr int kBatch = 16;
     for (int64_t n0 = n_begin; n0 < n_end; n0 += kBatch) {
         int kk[kBatch];
         float xv[kBatch];
         float gv[kBatch];
+        uint32_t mv[kBatch];
 #pragma unroll
         for (int t = 0; t < kBatch; ++t) {
             const int64_t n = n0 + t;
@@ -714,6 +810,7 @@ __global__ __launch_bounds__(kWave) void ple_bwd_simple_hist_kernel(BwdArgs a) {
             kk[t] = ok ? clamp_bin(load_idx<IdxT>(a.idx, p), n_real) : 0;
             xv[t] = ok ? a.x[p] : 0.0f;
             gv[t] = (ok && jok) ? load_grad<GD>(a.g, p * D + j) : 0.0f;
+            mv[t] = (ok && jok && a.mask) ? a.mask[p * a.MW + (j >> 5)] : ~0u;
         }
 #pragma unroll
         for (int t = 0; t < kBatch; ++t) {
@@ -721,7 +818,10 @@ __global__ __launch_bounds__(kWave) void ple_bwd_simple_hist_kernel(BwdArgs a) {
             const int k = kk[t];
             const float qf = quant<Q>((xv[t] - e[k]) * iwr[k]);
             const float graw = gv[t];
-            const float gq = quant<Q>(graw);
+            // ReLU epilogue: the forward's pass bit; linear0 sums use the raw g
+            const float gm = ((mv[t] >> (j & 31)) & 1u) ? graw : 0.0f;
+            const float gq = quant<Q>(gm);
+            if (a.lin_w) clw = fmaf(graw, xv[t], clw);
             if (k != kc) {
                 if (kc >= 0 && jok) {
                     hb[kc * D + j] += cb;
@@ -734,7 +834,7 @@ __global__ __launch_bounds__(kWave) void ple_bwd_simple_hist_kernel(BwdArgs a) {
                 cb += gq;
                 cw = fmaf(qf, gq, cw);
             }
-            cdb += graw;
+            cdb += a.lin_w ? graw : gm;
         }
     }
     if (kc >= 0 && jok) {
@@ -750,6 +850,7 @@ __global__ __launch_bounds__(kWave) void ple_bwd_simple_hist_kernel(BwdArgs a) {
         dst[k * 2 * D + D + jj] = hw[i];
     }
     if (jok) a.part_db[(static_cast<int64_t>(c) * F + f) * D + j] = cdb;
+    if (jok && a.lin_w) a.part_lw[(static_cast<int64_t>(c) * F + f) * D + j] = clw;
 }
 
 // ---------------------------------------------------------------------------
@@ -817,6 +918,11 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
                 for (int cc = 0; cc < a.Cd; ++cc) sb += a.part_db[(static_cast<int64_t>(cc) * F + f) * D + j];
             }
             a.db[static_cast<int64_t>(f) * D + j] = sb;
+        }
+        if (a.dlw) {
+            float sl = 0.0f;
+            for (int cc = 0; cc < a.Cd; ++cc) sl += a.part_lw[(static_cast<int64_t>(cc) * F + f) * D + j];
+            a.dlw[static_cast<int64_t>(f) * D + j] = sl;
         }
     }
 }
@@ -891,10 +997,11 @@ struct BwdPlan {
     int C, Cd;
     int64_t NC;
     size_t lds, sort_lds;
-    size_t part_bytes, part_db_bytes, desc_bytes, piece_bytes, npc_bytes, dxt_bytes;
+    size_t part_bytes, part_db_bytes, part_lw_bytes, desc_bytes, piece_bytes, npc_bytes, dxt_bytes;
     BwdArgs geo;     // sorted-path geometry and LDS offsets
     size_t total() const {
-        return align_up(part_bytes, 256) + align_up(part_db_bytes, 256) + align_up(desc_bytes, 256) +
+        return align_up(part_bytes, 256) + align_up(part_db_bytes, 256) + align_up(part_lw_bytes, 256) +
+               align_up(desc_bytes, 256) +
                align_up(piece_bytes, 256) + align_up(npc_bytes, 256) + align_up(dxt_bytes, 256);
     }
 };
@@ -923,8 +1030,9 @@ size_t sort_layout(BwdArgs &g, int FS, int B, int PM) {
     return take.off;
 }
 
-// raw_db: records carry the raw-gradient bias sums too (quantised gradients)
-size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_db) {
+// raw_db: records carry the raw-gradient bias sums too (quantised gradients,
+// linear0 epilogue); lin: and the linear0 weight sums
+size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_db, bool lin) {
     LdsTaker take;
     take(g.ro_qw, 4ull * FS * B * D);
     take(g.ro_hist, 8ull * FS * B * D);
@@ -934,16 +1042,18 @@ size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_
     take(g.ro_desc, 8ull * (kP + 1));
     take(g.ro_piece, 4ull * PM);
     take(g.ro_npc, 4);
-    take(g.ro_rec, (raw_db ? 12ull : 8ull) * LG * D);
+    take(g.ro_rec, (8ull + (raw_db ? 4ull : 0ull) + (lin ? 4ull : 0ull)) * LG * D);
     take(g.ro_rkey, 4ull * LG);
     take(g.ro_rfl, 4ull * LG);
     take(g.ro_dx, 4ull * (kP + 1));
     take(g.ro_inv, 2ull * kP);
+    take(g.ro_lw, lin ? 4ull * FS * D : 0ull);
+    take(g.ro_dlw, lin ? 4ull * FS * D : 0ull);
     return take.off;
 }
 
 // g_align16: the gradient's base address is 16-byte aligned
-BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16, bool raw_db) {
+BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16, bool raw_db, bool lin) {
     BwdPlan pl{};
     const int cus = device_cu_count();
     pl.sorted = false;
@@ -956,7 +1066,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
         // power-of-two width
         int vec = !g_align16 ? 1 : (D % 4 == 0 ? 4 : 1);
         const int vec_env = env_int("PLE_BWD_VEC", 0);    // tuning: 8 or 1 instead of the default
-        if (vec_env == 8 && D % 8 == 0 && g_align16) vec = 8;
+        if (vec_env == 8 && D % 8 == 0 && g_align16 && !lin) vec = 8;
         if (vec_env == 1) vec = 1;
         const int uv = static_cast<int>(D / vec);
         int lgw = 2;
@@ -970,7 +1080,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
             for (int fs = 4; fs >= 1; fs /= 2) {
                 if (fs > 1 && fs > F) continue;
                 BwdArgs t{};
-                const size_t lds = reduce_layout(t, fs, static_cast<int>(B), static_cast<int>(D), LG, pm_for(fs), raw_db);
+                const size_t lds = reduce_layout(t, fs, static_cast<int>(B), static_cast<int>(D), LG, pm_for(fs), raw_db, lin);
                 if (lds <= kReduceLdsTarget || (fs == 1 && lds <= kLdsMax)) {
                     best_fs = fs;
                     best_lds = lds;
@@ -981,7 +1091,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
             const int fs_env = env_int("PLE_BWD_FS", 0);
             if (fs_env == 1 || fs_env == 2 || fs_env == 4 || fs_env == 8 || fs_env == 16) {
                 BwdArgs t{};
-                const size_t lds = reduce_layout(t, fs_env, static_cast<int>(B), static_cast<int>(D), LG, pm_for(fs_env), raw_db);
+                const size_t lds = reduce_layout(t, fs_env, static_cast<int>(B), static_cast<int>(D), LG, pm_for(fs_env), raw_db, lin);
                 if (lds <= kLdsMax) {
                     best_fs = fs_env;
                     best_lds = lds;
@@ -1042,6 +1152,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
     }
     pl.part_bytes = static_cast<size_t>(pl.Cd) * F * B * 2 * D * sizeof(float);
     pl.part_db_bytes = static_cast<size_t>(pl.Cd) * F * D * sizeof(float);
+    pl.part_lw_bytes = lin ? static_cast<size_t>(pl.Cd) * F * D * sizeof(float) : 0;
     return pl;
 }
 
@@ -1055,22 +1166,45 @@ hipError_t launch_sort(const BwdArgs &a, int idxb, dim3 grid, size_t lds, hipStr
 
 // Lane-group width as a template argument for the 8- and 4-float rows (DPP
 // reductions); the one-column-per-lane variant takes it at run time.
+template <int GD, int Q, int EPI>
+hipError_t launch_reduce_epi(const BwdArgs &a, int vec, dim3 grid, size_t lds, hipStream_t s) {
+    if (vec == 4) {
+        switch (a.LGW) {
+            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 4, EPI>), grid, dim3(kBlock), lds, s, a); break;
+            case 8: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 8, EPI>), grid, dim3(kBlock), lds, s, a); break;
+            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 16, EPI>), grid, dim3(kBlock), lds, s, a); break;
+        }
+    } else {
+        hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 0, EPI>), grid, dim3(kBlock), lds, s, a);
+    }
+    return hipGetLastError();
+}
+
 template <int GD, int Q>
-hipError_t launch_reduce(const BwdArgs &a, int vec, dim3 grid, size_t lds, hipStream_t s) {
+hipError_t launch_reduce(const BwdArgs &a, int vec, int epi, dim3 grid, size_t lds, hipStream_t s) {
+    if constexpr (GD == PLE_DTYPE_F32) {
+        // module epilogues (their gradient is fp32); no 8-float rows
+        switch (epi) {
+            case kBwdRelu: return launch_reduce_epi<GD, Q, kBwdRelu>(a, vec, grid, lds, s);
+            case kBwdLin: return launch_reduce_epi<GD, Q, kBwdLin>(a, vec, grid, lds, s);
+            case kBwdLin | kBwdRelu: return launch_reduce_epi<GD, Q, kBwdLin | kBwdRelu>(a, vec, grid, lds, s);
+            default: break;
+        }
+    }
     if (vec == 8) {
         switch (a.LGW) {
-            case 2: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 2>), grid, dim3(kBlock), lds, s, a); break;
-            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 4>), grid, dim3(kBlock), lds, s, a); break;
-            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 8>), grid, dim3(kBlock), lds, s, a); break;
+            case 2: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 2, 0>), grid, dim3(kBlock), lds, s, a); break;
+            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 4, 0>), grid, dim3(kBlock), lds, s, a); break;
+            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 8, 0>), grid, dim3(kBlock), lds, s, a); break;
         }
     } else if (vec == 4) {
         switch (a.LGW) {
-            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 4>), grid, dim3(kBlock), lds, s, a); break;
-            case 8: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 8>), grid, dim3(kBlock), lds, s, a); break;
-            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 16>), grid, dim3(kBlock), lds, s, a); break;
+            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 4, 0>), grid, dim3(kBlock), lds, s, a); break;
+            case 8: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 8, 0>), grid, dim3(kBlock), lds, s, a); break;
+            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 16, 0>), grid, dim3(kBlock), lds, s, a); break;
         }
     } else {
-        hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 0>), grid, dim3(kBlock), lds, s, a);
+        hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 0, 0>), grid, dim3(kBlock), lds, s, a);
     }
     return hipGetLastError();
 }
@@ -1078,11 +1212,12 @@ hipError_t launch_reduce(const BwdArgs &a, int vec, dim3 grid, size_t lds, hipSt
 template <int GD, int Q>
 hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bool want_dwdb, hipStream_t s) {
     hipError_t e = hipSuccess;
+    const int epi = (a.mask ? kBwdRelu : 0) | (a.lin_w ? kBwdLin : 0);
     if (pl.sorted) {
-        a.db_from_buckets = Q == PLE_DTYPE_F32;
+        a.db_from_buckets = Q == PLE_DTYPE_F32 && a.lin_w == nullptr;
         e = launch_sort<Q>(a, idxb, dim3(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, a.T))), pl.sort_lds, s);
         if (e != hipSuccess) return e;
-        e = launch_reduce<GD, Q>(a, pl.vec, dim3(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, pl.C))), pl.lds, s);
+        e = launch_reduce<GD, Q>(a, pl.vec, epi, dim3(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, pl.C))), pl.lds, s);
         if (e != hipSuccess) return e;
         if (a.dxt) {
             const dim3 tg(static_cast<unsigned>((a.N + kTr - 1) / kTr), static_cast<unsigned>((a.F + kTr - 1) / kTr));
@@ -1143,23 +1278,30 @@ hipError_t launch_q(const BwdArgs &a, const BwdPlan &pl, int q, int idxb, bool w
 
 size_t backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D) {
     // the plan depends on the gradient's alignment and dtype; report the largest need
+    // (and on the epilogue: the linear0 sums need their own partials)
     size_t need = 0;
     for (int al = 0; al < 2; ++al)
-        for (int raw = 0; raw < 2; ++raw) {
-            const size_t t = plan_backward(N, F, B, D, al != 0, raw != 0).total();
-            need = t > need ? t : need;
-        }
+        for (int raw = 0; raw < 2; ++raw)
+            for (int lin = 0; lin <= raw; ++lin) {
+                const size_t t = plan_backward(N, F, B, D, al != 0, raw != 0, lin != 0).total();
+                need = t > need ? t : need;
+            }
     return need;
 }
 
 int backward_run(const BackwardRequest &r) {
+    const bool lin = r.lin_w != nullptr;
     const bool want_dx = r.dx != nullptr;
-    const bool want_dwdb = r.dw != nullptr || r.db != nullptr;
+    const bool want_dwdb = r.dw != nullptr || r.db != nullptr || r.dlw != nullptr;
     if (r.grad_dtype != PLE_DTYPE_F32 && r.quant != r.grad_dtype) return PLE_E_UNSUPPORTED;
+    // module epilogues: fp32 gradient; a ReLU needs the forward's bits
+    if ((r.relu || lin) && r.grad_dtype != PLE_DTYPE_F32) return PLE_E_UNSUPPORTED;
+    if (r.relu && !r.mask) return PLE_E_NULL_POINTER;
+    if (r.dlw && !lin) return PLE_E_UNSUPPORTED;
     const uintptr_t gaddr = reinterpret_cast<uintptr_t>(r.g);
     const int gbytes = r.grad_dtype == PLE_DTYPE_F32 ? 4 : 2;
     if (gaddr % gbytes != 0) return PLE_E_MISALIGNED;
-    BwdPlan pl = plan_backward(r.N, r.F, r.B, r.D, gaddr % 16 == 0, r.quant != PLE_DTYPE_F32);
+    BwdPlan pl = plan_backward(r.N, r.F, r.B, r.D, gaddr % 16 == 0, r.quant != PLE_DTYPE_F32 || lin, lin);
     if (!pl.sorted && want_dwdb && pl.lds > kLdsMax) return PLE_E_UNSUPPORTED;
     // the sorted path always needs its descriptors; the fallback only for dW / db
     const size_t need = (pl.sorted || want_dwdb) ? pl.total() : 0;
@@ -1172,6 +1314,8 @@ int backward_run(const BackwardRequest &r) {
     BwdArgs a = pl.geo;
     a.g = r.g; a.x = r.x; a.edges = r.edges; a.iw = r.iw; a.nbins = r.nbins; a.weight = r.weight;
     a.idx = r.idx; a.dx = r.dx; a.dw = r.dw; a.db = r.db;
+    a.mask = r.relu ? r.mask : nullptr; a.MW = static_cast<int>((r.D + 31) / 32);
+    a.lin_w = r.lin_w; a.dlw = r.dlw;
     char *ws = static_cast<char *>(r.workspace);
     size_t off = 0;
     auto carve = [&](size_t bytes) {
@@ -1181,8 +1325,10 @@ int backward_run(const BackwardRequest &r) {
     };
     float *part = reinterpret_cast<float *>(carve(pl.part_bytes));
     float *part_db = reinterpret_cast<float *>(carve(pl.part_db_bytes));
+    float *part_lw = reinterpret_cast<float *>(carve(pl.part_lw_bytes));
     a.part = want_dwdb ? part : nullptr;
     a.part_db = want_dwdb ? part_db : nullptr;
+    a.part_lw = want_dwdb && lin ? part_lw : nullptr;
     if (pl.sorted) {
         a.desc = reinterpret_cast<uint2 *>(carve(pl.desc_bytes));
         a.piece = reinterpret_cast<uint32_t *>(carve(pl.piece_bytes));

@@ -33,7 +33,7 @@ int check_common(int64_t N, int64_t F, int64_t B, int64_t D) {
 
 extern "C" {
 
-int ple_abi_version(void) { return (1 << 16) | 0; }
+int ple_abi_version(void) { return (1 << 16) | 1; }
 
 int ple_bin_index_bytes(int64_t max_n_bins) { return ple::idx_bytes_for(max_n_bins); }
 
@@ -103,6 +103,70 @@ int ple_backward_launch(const void *grad_output, const float *x, const float *bi
     r.weight = weight; r.idx = bin_indices; r.dx = grad_x; r.dw = grad_weight; r.db = grad_bias;
     r.N = N; r.F = F; r.B = B; r.D = D;
     r.grad_dtype = grad_dtype; r.quant = quant_dtype;
+    r.workspace = workspace; r.workspace_bytes = workspace_bytes;
+    r.stream = s;
+    return ple::backward_run(r);
+}
+
+int ple_forward_epilogue_launch(const float *x, const float *bin_edges, const float *inv_bin_widths,
+                                const int32_t *n_bins, const float *weight,
+                                const ple_epilogue_t *epilogue, float *output, void *bin_indices,
+                                int64_t N, int64_t F, int64_t B, int64_t D, int quant_dtype,
+                                void *stream) {
+    const int rc = ple::check_common(N, F, B, D);
+    if (rc != PLE_OK) return rc;
+    if (!ple::valid_dtype(quant_dtype)) return PLE_E_BAD_DTYPE;
+    if (!epilogue) return PLE_E_NULL_POINTER;
+    if ((epilogue->bias != nullptr) == (epilogue->lin_weight != nullptr)) return PLE_E_UNSUPPORTED;
+    if (epilogue->lin_weight && !epilogue->lin_bias) return PLE_E_NULL_POINTER;
+    if (N == 0) return PLE_OK;
+    if (!x || !bin_edges || !inv_bin_widths || !n_bins || !weight || !output || !bin_indices)
+        return PLE_E_NULL_POINTER;
+    ple::ForwardRequest r;
+    r.x = x; r.edges = bin_edges; r.iw = inv_bin_widths; r.nbins = n_bins; r.weight = weight;
+    r.bias = epilogue->bias; r.lin_w = epilogue->lin_weight; r.lin_b = epilogue->lin_bias;
+    r.relu = epilogue->relu ? 1 : 0; r.mask = epilogue->relu_mask;
+    r.out = output; r.idx = bin_indices;
+    r.N = N; r.F = F; r.B = B; r.D = D;
+    r.quant = quant_dtype; r.out_dtype = PLE_DTYPE_F32;
+    r.stream = static_cast<hipStream_t>(stream);
+    return ple::forward_run(r);
+}
+
+int ple_backward_epilogue_launch(const float *grad_output, const float *x, const float *bin_edges,
+                                 const float *inv_bin_widths, const int32_t *n_bins,
+                                 const float *weight, const void *bin_indices,
+                                 const ple_epilogue_t *epilogue, float *grad_x, float *grad_weight,
+                                 float *grad_bias, float *grad_lin_weight, float *grad_lin_bias,
+                                 int64_t N, int64_t F, int64_t B, int64_t D, int quant_dtype,
+                                 void *workspace, size_t workspace_bytes, void *stream) {
+    const int rc = ple::check_common(N, F, B, D);
+    if (rc != PLE_OK) return rc;
+    if (!ple::valid_dtype(quant_dtype)) return PLE_E_BAD_DTYPE;
+    if (!epilogue) return PLE_E_NULL_POINTER;
+    const bool lin = epilogue->lin_weight != nullptr;   // else version A (bias, lin_bias: not read)
+    if (lin ? grad_bias != nullptr : (grad_lin_weight != nullptr || grad_lin_bias != nullptr))
+        return PLE_E_UNSUPPORTED;
+    float *db = lin ? grad_lin_bias : grad_bias;
+    if (!grad_x && !grad_weight && !db && !grad_lin_weight) return PLE_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (N == 0) {
+        hipError_t e = hipSuccess;
+        if (grad_weight) e = hipMemsetAsync(grad_weight, 0, sizeof(float) * F * B * D, s);
+        if (e == hipSuccess && db) e = hipMemsetAsync(db, 0, sizeof(float) * F * D, s);
+        if (e == hipSuccess && grad_lin_weight) e = hipMemsetAsync(grad_lin_weight, 0, sizeof(float) * F * D, s);
+        return e == hipSuccess ? PLE_OK : static_cast<int>(e);
+    }
+    if (!grad_output || !x || !bin_edges || !inv_bin_widths || !n_bins || !weight || !bin_indices)
+        return PLE_E_NULL_POINTER;
+    if (epilogue->relu && !epilogue->relu_mask) return PLE_E_NULL_POINTER;
+    ple::BackwardRequest r;
+    r.g = grad_output; r.x = x; r.edges = bin_edges; r.iw = inv_bin_widths; r.nbins = n_bins;
+    r.weight = weight; r.idx = bin_indices; r.dx = grad_x; r.dw = grad_weight; r.db = db;
+    r.relu = epilogue->relu ? 1 : 0; r.mask = epilogue->relu_mask;
+    r.lin_w = epilogue->lin_weight; r.dlw = grad_lin_weight;
+    r.N = N; r.F = F; r.B = B; r.D = D;
+    r.grad_dtype = PLE_DTYPE_F32; r.quant = quant_dtype;
     r.workspace = workspace; r.workspace_bytes = workspace_bytes;
     r.stream = s;
     return ple::backward_run(r);

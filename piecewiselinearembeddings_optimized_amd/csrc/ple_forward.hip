@@ -10,8 +10,16 @@
 //
 // Arithmetic per output element is the reference's (forward_cuda.cu:135-178,
 // 208-283): prefix accumulated in fp32 in bin order, then
-// fma(q(frac), q(W[phys(k)]), prefix[k]), rounded to the output dtype; the
-// optional bias is added in fp32 after that rounding.
+// fma(q(frac), q(W[phys(k)]), prefix[k]), rounded to the output dtype.
+//
+// Epilogues (the module's elementwise tail, reference module.py:230-248,
+// fused into the store; the output is then fp32):
+//   bias       v = x_ple + bias                      (version A)
+//   bias_relu  v = relu(x_ple + bias)
+//   lin        v = (lin_b + lin_w * x) + x_ple        (version B, linear0)
+//   lin_relu   v = (lin_b + lin_w * x) + relu(x_ple)
+// With ReLU the store also writes one bit per element, set where the ReLU
+// passes its input (input > 0, or NaN), for the backward.
 
 #include <stdlib.h>
 
@@ -28,6 +36,10 @@ struct FwdArgs {
     const int32_t *nbins;
     const float *weight;
     const float *bias;
+    const float *lin_w;     // [F, D] linear0 weight (version B) or NULL
+    const float *lin_b;     // [F, D] linear0 bias
+    uint32_t *mask;         // [N, F, MW] ReLU pass bits, or NULL
+    int MW;                 // mask words per (sample, feature) row = ceil(D / 32)
     void *out;
     void *idx;
     int64_t N;
@@ -47,8 +59,25 @@ size_t fwd_lds_bytes(int FS, int B, int D) {
 
 constexpr int kStoreUnroll = 4;
 
-template <int Q, int OUT, bool HAS_BIAS, int VEC, typename IdxT>
+enum : int { kEpiNone = 0, kEpiBias = 1, kEpiBiasRelu = 2, kEpiLin = 3, kEpiLinRelu = 4 };
+
+// OR of v over the U consecutive lanes of a row (first lane: lane - u); every
+// lane of the row receives it.  Power-of-two rows are aligned to U lanes.
+__device__ __forceinline__ uint32_t row_or(uint32_t v, int U, int lane, int u) {
+    if ((U & (U - 1)) == 0) {
+        for (int off = 1; off < U; off <<= 1) v |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off));
+        return v;
+    }
+    uint32_t acc = 0;
+    for (int j = 0; j < U; ++j) acc |= static_cast<uint32_t>(__shfl(static_cast<int>(v), lane - u + j));
+    return acc;
+}
+
+template <int Q, int OUT, int EPI, int VEC, typename IdxT>
 __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
+    constexpr bool HAS_BIAS = EPI == kEpiBias || EPI == kEpiBiasRelu;
+    constexpr bool RELU = EPI == kEpiBiasRelu || EPI == kEpiLinRelu;
+    constexpr bool LIN = EPI == kEpiLin || EPI == kEpiLinRelu;
     extern __shared__ float smem[];
     const int FS = a.FS, B = a.B, D = a.D, F = a.F;
     const int rs = 2 * D;                                   // table row stride
@@ -153,16 +182,24 @@ __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
     const int o_fl = o_v / U;
     const int o_u = o_v - o_fl * U;
     const bool o_ok = (o_s < R) && (o_fl < nfh);
-    float bvec[VEC];
+    // per-lane epilogue parameters: bias, or linear0's weight and bias
+    float bvec[VEC], lwv[VEC];
 #pragma unroll
-    for (int t = 0; t < VEC; ++t) bvec[t] = 0.0f;
-    if constexpr (HAS_BIAS) {
+    for (int t = 0; t < VEC; ++t) bvec[t] = lwv[t] = 0.0f;
+    if constexpr (HAS_BIAS || LIN) {
         if (o_ok) {
+            const int64_t pofs = static_cast<int64_t>(f0 + o_fl) * D + o_u * VEC;
 #pragma unroll
-            for (int t = 0; t < VEC; ++t)
-                bvec[t] = a.bias[static_cast<int64_t>(f0 + o_fl) * D + o_u * VEC + t];
+            for (int t = 0; t < VEC; ++t) {
+                bvec[t] = HAS_BIAS ? a.bias[pofs + t] : a.lin_b[pofs + t];
+                if constexpr (LIN) lwv[t] = a.lin_w[pofs + t];
+            }
         }
     }
+    // ReLU bits: element j of a row is bit j % 32 of word j / 32 (a lane's
+    // VEC elements never straddle a word: VEC divides 32)
+    const int m_shift = (o_u * VEC) & 31;
+    const int m_word = (o_u * VEC) >> 5;
     const float *o_tbl = tbl + static_cast<size_t>(o_fl) * B * rs + o_u * VEC;
 
     const int64_t rows = n_end - n_begin;
@@ -195,12 +232,13 @@ __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
         // reads are issued together, then the stores
         for (int sb = 0; sb < SW; sb += R * kStoreUnroll) {
             int ks[kStoreUnroll];
-            float qs[kStoreUnroll];
+            float qs[kStoreUnroll], xs[kStoreUnroll];
 #pragma unroll
             for (int q = 0; q < kStoreUnroll; ++q) {
                 const int src = ((sb + q * R + o_s) * FS + o_fl) & (kWave - 1);
                 ks[q] = __shfl(k, src);
                 qs[q] = __shfl(qf, src);
+                if constexpr (LIN) xs[q] = __shfl(v, src);
             }
 #pragma unroll
             for (int q = 0; q < kStoreUnroll; ++q) {
@@ -218,14 +256,34 @@ __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
                 } else {
                     r[0] = fmaf(qs[q], row[D], row[0]);
                 }
+                uint32_t mbits = 0;
 #pragma unroll
                 for (int t2 = 0; t2 < VEC; ++t2) {
                     float o = quant<Q>(r[t2]);
                     if constexpr (HAS_BIAS) o = o + bvec[t2];
+                    if constexpr (RELU) {
+                        // torch.relu: NaN passes, x <= 0 gives 0
+                        const bool pass = !(o <= 0.0f);
+                        mbits |= static_cast<uint32_t>(pass) << t2;
+                        o = pass ? o : 0.0f;
+                    }
+                    if constexpr (LIN) o = fmaf(lwv[t2], xs[q], bvec[t2]) + o;
                     r[t2] = o;
                 }
-                if (o_ok && s < SW && n < n_end)
+                const bool row_ok = o_ok && s < SW && n < n_end;
+                if (row_ok)
                     store_out<OUT, VEC>(a.out, n * row_elems + static_cast<int64_t>(f0 + o_fl) * D + o_u * VEC, r);
+                if constexpr (RELU) {
+                    if (a.mask) {
+                        const uint32_t w0 = row_or(m_word == 0 ? mbits << m_shift : 0u, U, lane, o_u);
+                        const uint32_t w1 = a.MW > 1 ? row_or(m_word == 1 ? mbits << m_shift : 0u, U, lane, o_u) : 0u;
+                        if (row_ok && o_u == 0) {
+                            uint32_t *mp = a.mask + (n * F + f0 + o_fl) * a.MW;
+                            mp[0] = w0;
+                            if (a.MW > 1) mp[1] = w1;
+                        }
+                    }
+                }
             }
         }
     }
@@ -278,32 +336,43 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, bool aligned16, Fw
     return true;
 }
 
-template <int Q, int OUT, bool HB, int VEC>
+template <int Q, int OUT, int EPI, int VEC>
 hipError_t launch_idx(const FwdArgs &a, int idxb, dim3 grid, size_t lds, hipStream_t s) {
     // uint8 indices up to 256 bins, int16 beyond (at most 32766 bins)
-    if (idxb == 1) hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, HB, VEC, uint8_t>), grid, dim3(kBlock), lds, s, a);
-    else hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, HB, VEC, int16_t>), grid, dim3(kBlock), lds, s, a);
+    if (idxb == 1) hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, uint8_t>), grid, dim3(kBlock), lds, s, a);
+    else hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, int16_t>), grid, dim3(kBlock), lds, s, a);
     return hipGetLastError();
 }
 
-template <int Q, int OUT, bool HB>
+template <int Q, int OUT, int EPI>
 hipError_t launch_vec(const FwdArgs &a, int vec, int idxb, dim3 grid, size_t lds, hipStream_t s) {
-    return vec == 4 ? launch_idx<Q, OUT, HB, 4>(a, idxb, grid, lds, s)
-                    : launch_idx<Q, OUT, HB, 1>(a, idxb, grid, lds, s);
+    return vec == 4 ? launch_idx<Q, OUT, EPI, 4>(a, idxb, grid, lds, s)
+                    : launch_idx<Q, OUT, EPI, 1>(a, idxb, grid, lds, s);
 }
 
-// Supported (quant, output) pairs: output == quant without bias (the
-// reference operator), output == F32 with bias (the fused module epilogue).
+// Supported (quant, output) pairs: output == quant without an epilogue (the
+// reference operator), output == F32 with one (the fused module tail).
 template <int Q>
-hipError_t launch_q(const FwdArgs &a, int vec, int idxb, dim3 grid, size_t lds, hipStream_t s) {
-    if (a.bias) return launch_vec<Q, PLE_DTYPE_F32, true>(a, vec, idxb, grid, lds, s);
-    return launch_vec<Q, Q, false>(a, vec, idxb, grid, lds, s);
+hipError_t launch_q(const FwdArgs &a, int epi, int vec, int idxb, dim3 grid, size_t lds, hipStream_t s) {
+    switch (epi) {
+        case kEpiBias: return launch_vec<Q, PLE_DTYPE_F32, kEpiBias>(a, vec, idxb, grid, lds, s);
+        case kEpiBiasRelu: return launch_vec<Q, PLE_DTYPE_F32, kEpiBiasRelu>(a, vec, idxb, grid, lds, s);
+        case kEpiLin: return launch_vec<Q, PLE_DTYPE_F32, kEpiLin>(a, vec, idxb, grid, lds, s);
+        case kEpiLinRelu: return launch_vec<Q, PLE_DTYPE_F32, kEpiLinRelu>(a, vec, idxb, grid, lds, s);
+        default: return launch_vec<Q, Q, kEpiNone>(a, vec, idxb, grid, lds, s);
+    }
 }
 
 }  // namespace
 
 int forward_run(const ForwardRequest &r) {
-    if (r.bias ? r.out_dtype != PLE_DTYPE_F32 : r.out_dtype != r.quant) return PLE_E_UNSUPPORTED;
+    // epilogue: bias (+ ReLU) or linear0 (+ ReLU); never both, ReLU needs one
+    if (r.bias && r.lin_w) return PLE_E_UNSUPPORTED;
+    if (r.lin_w && !r.lin_b) return PLE_E_NULL_POINTER;
+    if (r.relu && !r.bias && !r.lin_w) return PLE_E_UNSUPPORTED;
+    const int epi = r.bias ? (r.relu ? kEpiBiasRelu : kEpiBias)
+                  : r.lin_w ? (r.relu ? kEpiLinRelu : kEpiLin) : kEpiNone;
+    if (epi != kEpiNone ? r.out_dtype != PLE_DTYPE_F32 : r.out_dtype != r.quant) return PLE_E_UNSUPPORTED;
     const int out_bytes = r.out_dtype == PLE_DTYPE_F32 ? 4 : 2;
     if (reinterpret_cast<uintptr_t>(r.out) % out_bytes != 0) return PLE_E_MISALIGNED;
     const bool aligned16 = (reinterpret_cast<uintptr_t>(r.out) % (4 * out_bytes) == 0) &&
@@ -312,7 +381,9 @@ int forward_run(const ForwardRequest &r) {
     if (!plan_forward(r.N, r.F, r.B, r.D, aligned16, pl)) return PLE_E_UNSUPPORTED;
     FwdArgs a;
     a.x = r.x; a.edges = r.edges; a.iw = r.iw; a.nbins = r.nbins; a.weight = r.weight;
-    a.bias = r.bias; a.out = r.out; a.idx = r.idx;
+    a.bias = r.bias; a.lin_w = r.lin_w; a.lin_b = r.lin_b;
+    a.mask = r.relu ? r.mask : nullptr; a.MW = static_cast<int>((r.D + 31) / 32);
+    a.out = r.out; a.idx = r.idx;
     a.N = r.N; a.F = static_cast<int>(r.F); a.B = static_cast<int>(r.B); a.D = static_cast<int>(r.D);
     a.FS = pl.FS; a.G = pl.G; a.C = pl.C; a.NC = pl.NC;
     const int64_t grid = kNumXcd * tiles_per_xcd(pl.G, pl.C);
@@ -320,9 +391,9 @@ int forward_run(const ForwardRequest &r) {
     const int idxb = idx_bytes_for(r.B);
     hipError_t e;
     switch (r.quant) {
-        case PLE_DTYPE_F32: e = launch_q<PLE_DTYPE_F32>(a, pl.vec, idxb, dim3(grid), pl.lds, r.stream); break;
-        case PLE_DTYPE_F16: e = launch_q<PLE_DTYPE_F16>(a, pl.vec, idxb, dim3(grid), pl.lds, r.stream); break;
-        default: e = launch_q<PLE_DTYPE_BF16>(a, pl.vec, idxb, dim3(grid), pl.lds, r.stream); break;
+        case PLE_DTYPE_F32: e = launch_q<PLE_DTYPE_F32>(a, epi, pl.vec, idxb, dim3(grid), pl.lds, r.stream); break;
+        case PLE_DTYPE_F16: e = launch_q<PLE_DTYPE_F16>(a, epi, pl.vec, idxb, dim3(grid), pl.lds, r.stream); break;
+        default: e = launch_q<PLE_DTYPE_BF16>(a, epi, pl.vec, idxb, dim3(grid), pl.lds, r.stream); break;
     }
     return e == hipSuccess ? PLE_OK : static_cast<int>(e);
 }

@@ -24,6 +24,9 @@ struct ForwardRequest {
     const float *x, *edges, *iw;
     const int32_t *nbins;
     const float *weight, *bias;
+    const float *lin_w = nullptr, *lin_b = nullptr;   // version-B linear0
+    int relu = 0;
+    uint32_t *mask = nullptr;                          // ReLU pass bits
     void *out, *idx;
     int64_t N, F, B, D;
     int quant, out_dtype;
@@ -40,6 +43,10 @@ struct BackwardRequest {
     const float *weight;
     const void *idx;
     float *dx, *dw, *db;
+    const uint32_t *mask = nullptr;    // ReLU pass bits of the forward
+    int relu = 0;
+    const float *lin_w = nullptr;      // version-B linear0 weight
+    float *dlw = nullptr;              // its gradient (db then holds linear0's bias gradient)
     int64_t N, F, B, D;
     int grad_dtype, quant;
     void *workspace;

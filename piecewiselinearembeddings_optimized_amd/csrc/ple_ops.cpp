@@ -14,7 +14,11 @@
 // `forward_with_bias` / `backward_with_bias` are this build's additions: the
 // same computation with the module's bias add fused into the output store
 // (reference module.py:238-239 does it as a separate PyTorch op) and the bias
-// gradient produced by the backward pass.
+// gradient produced by the backward pass.  `forward_epilogue` /
+// `backward_epilogue` fuse the module's whole tail (module.py:230-248): the
+// bias and ReLU of version A, or the ReLU and the linear0 residual of
+// version B; with ReLU the forward also returns one pass bit per element
+// (int32 words [N, F, ceil(D / 32)]) for the backward.
 
 #include <Python.h>
 
@@ -159,6 +163,52 @@ std::tuple<at::Tensor, at::Tensor> ple_forward_with_bias(const at::Tensor &x, co
     return run_forward(x, bin_edges, inv_bin_widths, n_bins, weight, &bias, quant_dtype, at::kFloat);
 }
 
+void check_param_fd(const at::Tensor &t, const at::Tensor &x, const at::Tensor &weight, const char *name) {
+    TORCH_CHECK(t.is_cuda() && t.device() == x.device(), name, " must be on the same CUDA device as x");
+    TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+    TORCH_CHECK(t.scalar_type() == at::kFloat, name, " must be float32");
+    TORCH_CHECK(t.dim() == 2 && t.size(0) == weight.size(0) && t.size(1) == weight.size(2), name,
+                " must have shape [F, D]");
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> ple_forward_epilogue(
+    const at::Tensor &x, const at::Tensor &bin_edges, const at::Tensor &inv_bin_widths,
+    const at::Tensor &n_bins, const at::Tensor &weight, const c10::optional<at::Tensor> &bias,
+    const c10::optional<at::Tensor> &lin_weight, const c10::optional<at::Tensor> &lin_bias, bool relu,
+    bool save_mask, at::ScalarType quant_dtype) {
+    check_forward_inputs(x, bin_edges, inv_bin_widths, n_bins, weight);
+    TORCH_CHECK(quant_dtype == at::kFloat || quant_dtype == at::kHalf || quant_dtype == at::kBFloat16,
+                "quant_dtype must be float32, float16, or bfloat16");
+    const bool has_bias = bias.has_value() && bias->defined();
+    const bool has_lin = lin_weight.has_value() && lin_weight->defined();
+    TORCH_CHECK(has_bias != has_lin, "exactly one of bias and lin_weight must be given");
+    if (has_bias) check_param_fd(*bias, x, weight, "bias");
+    if (has_lin) {
+        TORCH_CHECK(lin_bias.has_value() && lin_bias->defined(), "lin_bias must be given with lin_weight");
+        check_param_fd(*lin_weight, x, weight, "lin_weight");
+        check_param_fd(*lin_bias, x, weight, "lin_bias");
+    }
+    const int64_t N = x.size(0), F = x.size(1), B = weight.size(1), D = weight.size(2);
+    DeviceScope scope(x.device().index());
+    at::Tensor output = at::empty({N, F, D}, weight.options().dtype(at::kFloat));
+    at::Tensor bin_indices = at::empty({N, F}, weight.options().dtype(bin_index_scalar_type(B)));
+    at::Tensor mask = (relu && save_mask) ? at::empty({N, F, (D + 31) / 32}, weight.options().dtype(at::kInt))
+                                          : at::empty({0}, weight.options().dtype(at::kInt));
+    if (output.numel() == 0) return {output, bin_indices, mask};
+    ple_epilogue_t epi{};
+    epi.bias = has_bias ? bias->data_ptr<float>() : nullptr;
+    epi.lin_weight = has_lin ? lin_weight->data_ptr<float>() : nullptr;
+    epi.lin_bias = has_lin ? lin_bias->data_ptr<float>() : nullptr;
+    epi.relu = relu ? 1 : 0;
+    epi.relu_mask = mask.numel() > 0 ? reinterpret_cast<uint32_t *>(mask.data_ptr<int32_t>()) : nullptr;
+    const int rc = ple_forward_epilogue_launch(
+        x.data_ptr<float>(), bin_edges.data_ptr<float>(), inv_bin_widths.data_ptr<float>(),
+        n_bins.data_ptr<int32_t>(), weight.data_ptr<float>(), &epi, output.data_ptr<float>(),
+        bin_indices.data_ptr(), N, F, B, D, ple_dtype_of(quant_dtype), current_stream(x));
+    check_rc(rc, "ple_forward_epilogue_launch");
+    return {output, bin_indices, mask};
+}
+
 void check_backward_inputs(const at::Tensor &grad_output, const at::Tensor &x, const at::Tensor &bin_edges,
                            const at::Tensor &inv_bin_widths, const at::Tensor &n_bins,
                            const at::Tensor &weight, const at::Tensor &bin_indices) {
@@ -269,6 +319,62 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> ple_backward_with_bias(
                         compute_grad_x, compute_grad_weight, compute_grad_bias);
 }
 
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> ple_backward_epilogue(
+    const at::Tensor &grad_output, const at::Tensor &x, const at::Tensor &bin_edges,
+    const at::Tensor &inv_bin_widths, const at::Tensor &n_bins, const at::Tensor &weight,
+    const at::Tensor &bin_indices, const at::Tensor &relu_mask, const c10::optional<at::Tensor> &lin_weight,
+    bool relu, at::ScalarType quant_dtype, bool compute_grad_x, bool compute_grad_weight,
+    bool compute_grad_bias, bool compute_grad_lin_weight, bool compute_grad_lin_bias) {
+    check_backward_inputs(grad_output, x, bin_edges, inv_bin_widths, n_bins, weight, bin_indices);
+    TORCH_CHECK(grad_output.scalar_type() == at::kFloat, "grad_output must be float32");
+    TORCH_CHECK(quant_dtype == at::kFloat || quant_dtype == at::kHalf || quant_dtype == at::kBFloat16,
+                "quant_dtype must be float32, float16, or bfloat16");
+    const bool has_lin = lin_weight.has_value() && lin_weight->defined();
+    if (has_lin) check_param_fd(*lin_weight, x, weight, "lin_weight");
+    TORCH_CHECK(!(has_lin && compute_grad_bias), "no bias gradient with lin_weight (version B has no bias)");
+    TORCH_CHECK(has_lin || (!compute_grad_lin_weight && !compute_grad_lin_bias),
+                "linear0 gradients need lin_weight");
+    const int64_t N = x.size(0), F = x.size(1), B = weight.size(1), D = weight.size(2);
+    if (relu) {
+        TORCH_CHECK(relu_mask.is_cuda() && relu_mask.device() == x.device() && relu_mask.is_contiguous() &&
+                        relu_mask.scalar_type() == at::kInt && relu_mask.dim() == 3 && relu_mask.size(0) == N &&
+                        relu_mask.size(1) == F && relu_mask.size(2) == (D + 31) / 32,
+                    "relu_mask must be the int32 [N, F, ceil(D / 32)] pass bits of the forward");
+    }
+    DeviceScope scope(x.device().index());
+    auto fd = [&](bool want) {
+        return want ? (N == 0 ? at::zeros({F, D}, weight.options()) : at::empty({F, D}, weight.options()))
+                    : at::empty({0}, weight.options());
+    };
+    at::Tensor grad_x = compute_grad_x ? at::empty_like(x) : at::empty({0}, x.options());
+    at::Tensor grad_weight = compute_grad_weight ? (N == 0 ? at::zeros_like(weight) : at::empty_like(weight))
+                                                 : at::empty({0}, weight.options());
+    at::Tensor grad_bias = fd(compute_grad_bias);
+    at::Tensor grad_lw = fd(compute_grad_lin_weight);
+    at::Tensor grad_lb = fd(compute_grad_lin_bias);
+    if (N == 0 || (!compute_grad_x && !compute_grad_weight && !compute_grad_bias && !compute_grad_lin_weight &&
+                   !compute_grad_lin_bias))
+        return {grad_x, grad_weight, grad_bias, grad_lw, grad_lb};
+    const size_t ws_bytes = ple_backward_workspace_bytes(N, F, B, D);
+    at::Tensor workspace = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)}, x.options().dtype(at::kByte));
+    // version B when lin_weight is given, else version A
+    ple_epilogue_t epi{};
+    epi.lin_weight = has_lin ? lin_weight->data_ptr<float>() : nullptr;
+    epi.relu = relu ? 1 : 0;
+    epi.relu_mask = relu ? reinterpret_cast<uint32_t *>(relu_mask.data_ptr<int32_t>()) : nullptr;
+    const int rc = ple_backward_epilogue_launch(
+        grad_output.data_ptr<float>(), x.data_ptr<float>(), bin_edges.data_ptr<float>(),
+        inv_bin_widths.data_ptr<float>(), n_bins.data_ptr<int32_t>(), weight.data_ptr<float>(),
+        bin_indices.data_ptr(), &epi, compute_grad_x ? grad_x.data_ptr<float>() : nullptr,
+        compute_grad_weight ? grad_weight.data_ptr<float>() : nullptr,
+        compute_grad_bias ? grad_bias.data_ptr<float>() : nullptr,
+        compute_grad_lin_weight ? grad_lw.data_ptr<float>() : nullptr,
+        compute_grad_lin_bias ? grad_lb.data_ptr<float>() : nullptr, N, F, B, D, ple_dtype_of(quant_dtype),
+        workspace.data_ptr(), ws_bytes, current_stream(x));
+    check_rc(rc, "ple_backward_epilogue_launch");
+    return {grad_x, grad_weight, grad_bias, grad_lw, grad_lb};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(rtdl_num_embeddings_cuda, m) {
@@ -287,6 +393,16 @@ TORCH_LIBRARY(rtdl_num_embeddings_cuda, m) {
         "Tensor n_bins, Tensor weight, Tensor bin_indices, ScalarType quant_dtype, bool compute_grad_x, "
         "bool compute_grad_weight, bool compute_grad_bias) -> (Tensor grad_x, Tensor grad_weight, "
         "Tensor grad_bias)");
+    m.def(
+        "forward_epilogue(Tensor x, Tensor bin_edges, Tensor inv_bin_widths, Tensor n_bins, Tensor weight, "
+        "Tensor? bias, Tensor? lin_weight, Tensor? lin_bias, bool relu, bool save_mask, ScalarType quant_dtype) "
+        "-> (Tensor output, Tensor bin_indices, Tensor relu_mask)");
+    m.def(
+        "backward_epilogue(Tensor grad_output, Tensor x, Tensor bin_edges, Tensor inv_bin_widths, "
+        "Tensor n_bins, Tensor weight, Tensor bin_indices, Tensor relu_mask, Tensor? lin_weight, bool relu, "
+        "ScalarType quant_dtype, bool compute_grad_x, bool compute_grad_weight, bool compute_grad_bias, "
+        "bool compute_grad_lin_weight, bool compute_grad_lin_bias) -> (Tensor grad_x, Tensor grad_weight, "
+        "Tensor grad_bias, Tensor grad_lin_weight, Tensor grad_lin_bias)");
 }
 
 TORCH_LIBRARY_IMPL(rtdl_num_embeddings_cuda, CUDA, m) {
@@ -294,6 +410,8 @@ TORCH_LIBRARY_IMPL(rtdl_num_embeddings_cuda, CUDA, m) {
     m.impl("backward", &ple_backward);
     m.impl("forward_with_bias", &ple_forward_with_bias);
     m.impl("backward_with_bias", &ple_backward_with_bias);
+    m.impl("forward_epilogue", &ple_forward_epilogue);
+    m.impl("backward_epilogue", &ple_backward_epilogue);
 }
 
 // Importing the extension module runs the registrations above; the module

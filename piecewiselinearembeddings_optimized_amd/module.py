@@ -8,11 +8,16 @@ package is not a dependency here: its module structure -- ``linear0``
 layer), ``activation`` -- is restated in this file so parameter names, buffer
 names, initialisation order and the CPU computation stay the same.
 
-On a HIP device the PLE branch runs through the fused operators:
+On a HIP device the whole module runs through the fused operator
+``forward_epilogue`` (one forward kernel, one backward launch):
 
-* version A (bias) -> ``forward_with_bias``: bias add fused into the kernel's
-  store, bias gradient produced by the backward kernels;
-* version B (no bias) -> ``forward``, then ``x_linear + x_ple`` in PyTorch.
+* version A: ``relu?(x_ple + bias)`` fused into the kernel's store;
+* version B: ``linear0(x) + relu?(x_ple)`` fused into the store, linear0's
+  gradients produced by the same backward pass;
+* with ReLU the forward keeps one pass bit per element for the backward.
+
+Parameters that are not contiguous float32 ``[F, D]`` tensors fall back to
+``forward`` plus the same tail in PyTorch.
 
 Under CUDA/HIP autocast (float16 / bfloat16) the kernels round the fraction,
 the weights and the result through the autocast dtype with fp32 accumulation,
@@ -278,23 +283,36 @@ class CudaPiecewiseLinearEmbeddings(nn.Module):
         if x.device != self._cuda_bin_edges.device:
             raise RuntimeError("x and the module must be on the same CUDA device")
 
-        x_linear = None if self.linear0 is None else self.linear0(x)
         self._check_cuda_inputs(x)
         out_dtype = self._cuda_output_dtype()
         assert out_dtype in SUPPORTED_OUTPUT_DTYPES
         bias = self.linear.bias
-        if bias is not None and bias.dtype == torch.float32 and bias.is_contiguous():
-            x_ple, _ = _ops.forward_with_bias(
-                x, self._cuda_bin_edges, self._cuda_inv_bin_widths, self._cuda_n_bins,
-                self.linear.weight, bias, out_dtype,
+        l0 = self.linear0
+        shape_fd = (self.n_features, self.d_embedding)
+
+        def fusable(t) -> bool:
+            return t.dtype == torch.float32 and t.is_contiguous() and t.device == x.device and t.shape == shape_fd
+
+        if l0 is None and bias is not None and fusable(bias):
+            out, _, _ = _ops.forward_epilogue(
+                x, self._cuda_bin_edges, self._cuda_inv_bin_widths, self._cuda_n_bins, self.linear.weight,
+                bias, None, None, self.activation is not None, torch.is_grad_enabled(), out_dtype,
             )
-        else:
-            x_ple, _ = _ops.forward(
-                x, self._cuda_bin_edges, self._cuda_inv_bin_widths, self._cuda_n_bins,
-                self.linear.weight, out_dtype,
+            return out
+        if l0 is not None and bias is None and fusable(l0.weight) and fusable(l0.bias):
+            out, _, _ = _ops.forward_epilogue(
+                x, self._cuda_bin_edges, self._cuda_inv_bin_widths, self._cuda_n_bins, self.linear.weight,
+                None, l0.weight, l0.bias, self.activation is not None, torch.is_grad_enabled(), out_dtype,
             )
-            if bias is not None:
-                x_ple = x_ple + bias
+            return out
+
+        # unfused tail: the reference's sequence of PyTorch ops
+        x_linear = None if l0 is None else l0(x)
+        x_ple, _ = _ops.forward(
+            x, self._cuda_bin_edges, self._cuda_inv_bin_widths, self._cuda_n_bins, self.linear.weight, out_dtype,
+        )
+        if bias is not None:
+            x_ple = x_ple + bias
         if self.activation is not None:
             x_ple = self.activation(x_ple)
         return x_ple if x_linear is None else x_linear + x_ple

@@ -130,3 +130,34 @@ def test_compile_inductor_under_autocast():
         oc = compiled(x)
     assert oc.dtype == oe.dtype
     torch.testing.assert_close(oc.float(), oe.float(), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("version,relu", [("A", False), ("A", True), ("B", False), ("B", True)])
+def test_opcheck_forward_epilogue(version, relu):
+    w, x, e, iw, nb, wt, bt = _inputs()
+    f, d = wt.shape[0], wt.shape[2]
+    x.requires_grad_(True)
+    wt.requires_grad_(True)
+    if version == "A":
+        bias, lw, lb = bt.requires_grad_(True), None, None
+    else:
+        gen = torch.Generator(DEV).manual_seed(3)
+        bias = None
+        lw = torch.randn((f, d), device=DEV, generator=gen).requires_grad_(True)
+        lb = torch.randn((f, d), device=DEV, generator=gen).requires_grad_(True)
+    torch.library.opcheck(ops.forward_epilogue.default, (x, e, iw, nb, wt, bias, lw, lb, relu, True, torch.bfloat16))
+
+
+@pytest.mark.parametrize("version,relu", [("A", True), ("B", True)])
+def test_opcheck_backward_epilogue(version, relu):
+    w, x, e, iw, nb, wt, bt = _inputs()
+    n, f, _, d = w.shape
+    gen = torch.Generator(DEV).manual_seed(4)
+    lw = torch.randn((f, d), device=DEV, generator=gen) if version == "B" else None
+    lb = torch.randn((f, d), device=DEV, generator=gen) if version == "B" else None
+    _, idx, mask = ops.forward_epilogue(x, e, iw, nb, wt, bt if version == "A" else None, lw, lb, relu, True,
+                                        torch.float32)
+    g = torch.randn((n, f, d), device=DEV, generator=gen)
+    a = version == "A"
+    torch.library.opcheck(ops.backward_epilogue.default,
+                          (g, x, e, iw, nb, wt, idx, mask, lw, relu, torch.float32, True, True, a, not a, not a))

@@ -349,3 +349,58 @@ def test_c_backward_matches_numpy_oracle(c_oracle):
             got = c_oracle.backward_f64(g, x, edges, iw, nb, w, idx, quant=quant)
             for key in ("dx", "dw", "db", "dx_abs", "dw_abs", "db_abs"):
                 np.testing.assert_allclose(got[key], ref[key], rtol=1e-10, atol=1e-12, err_msg=key)
+
+
+# ---------------------------------------------------------------------------
+# module tail (bias / ReLU / version-B linear0): closed form vs torch autograd
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case_name", BIN_CASE_NAMES)
+@pytest.mark.parametrize("version,relu", [("A", False), ("A", True), ("B", False), ("B", True)])
+def test_module_tail_matches_torch_autograd(case_name, version, relu):
+    bins, x, edges, iw, nb, w, b, g = _case(case_name, 12, 31)
+    rng = np.random.default_rng(5)
+    f, d = w.shape[0], w.shape[2]
+    w0 = rng.uniform(-0.4, 0.4, size=(f, d)).astype(np.float32)
+    b0 = rng.uniform(-0.4, 0.4, size=(f, d)).astype(np.float32)
+    tables = (edges, iw, nb)
+    lin = (w0, b0) if version == "B" else None
+    bias = b if version == "A" else None
+    out, idx, pre = po.module_forward(x, tables, w, bias=bias, linear0=lin, activation=relu)
+    passm = po.relu_pass(pre) if relu else None
+    r = po.module_backward(g, x, tables, w, idx, pass_mask=passm, has_bias=version == "A", linear0=lin)
+
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    wt = torch.tensor(_dense_w(w, nb), dtype=torch.float64, requires_grad=True)
+    zero = torch.zeros((f, d), dtype=torch.float64)
+    bt = torch.tensor(b, dtype=torch.float64, requires_grad=True) if version == "A" else zero
+    v = _torch_dense_forward(xt, bins, wt, bt)
+    a = torch.relu(v) if relu else v
+    if version == "B":
+        w0t = torch.tensor(w0, dtype=torch.float64, requires_grad=True)
+        b0t = torch.tensor(b0, dtype=torch.float64, requires_grad=True)
+        a = torch.addcmul(b0t, w0t, xt[..., None]) + a
+    a.backward(torch.tensor(g, dtype=torch.float64))
+    np.testing.assert_allclose(out, a.detach().numpy(), rtol=2e-6, atol=2e-6)
+    np.testing.assert_allclose(r["dx"], xt.grad.numpy(), rtol=2e-6, atol=2e-6)
+    np.testing.assert_allclose(r["dw"], wt.grad.numpy(), rtol=2e-6, atol=2e-6)
+    if version == "A":
+        np.testing.assert_allclose(r["db"], bt.grad.numpy(), rtol=1e-12, atol=1e-12)
+        assert "dlw" not in r
+    else:
+        assert "db" not in r
+        np.testing.assert_allclose(r["dlw"], w0t.grad.numpy(), rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(r["dlb"], b0t.grad.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_pass_bits_pack_and_unpack():
+    rng = np.random.default_rng(3)
+    for d in (1, 10, 31, 32, 33, 64):
+        passm = rng.random((5, 3, d)) < 0.5
+        words = po.pack_pass_bits(passm)
+        assert words.dtype == np.int32 and words.shape == (5, 3, (d + 31) // 32)
+        np.testing.assert_array_equal(po.unpack_pass_bits(words, d), passm)
+        # bit j of the row sits at bit j % 32 of word j // 32
+        j = d - 1
+        np.testing.assert_array_equal((words.view(np.uint32)[..., j // 32] >> (j % 32)) & 1, passm[..., j])
+    assert po.relu_pass(np.array([np.nan, -0.0, 0.0, 1e-30, -1e-30])).tolist() == [True, False, False, True, False]
