@@ -17,9 +17,12 @@ from . import _C as _C  # noqa: F401
 from . import _meta as _meta  # noqa: F401
 from . import _autograd as _autograd  # noqa: F401
 from .module import CudaPiecewiseLinearEmbeddings
+from .bins import bin_tables, compute_bins
 
 __all__ = [
     "CudaPiecewiseLinearEmbeddings",
+    "bin_tables",
+    "compute_bins",
 ]
 
 __version__ = "0.2.0.dev0"

@@ -37,32 +37,11 @@ from torch import Tensor, nn
 from torch.nn.parameter import Parameter
 
 from ._meta import SUPPORTED_OUTPUT_DTYPES
+from .bins import bin_tables, check_bins
 
 _ops = torch.ops.rtdl_num_embeddings_cuda
 
 MAX_D_EMBEDDING = 64
-
-
-def check_bins(bins: list[Tensor]) -> None:
-    """Validate per-feature bin edges (upstream ``_check_bins``)."""
-    if not bins:
-        raise ValueError("The list of bins must not be empty")
-    for i, feature_bins in enumerate(bins):
-        if not isinstance(feature_bins, Tensor):
-            raise ValueError(f"bins must be a list of PyTorch tensors; bins[{i}] is {type(feature_bins)}")
-        if feature_bins.ndim != 1:
-            raise ValueError(f"Each item of the bin list must have exactly one dimension; bins[{i}].ndim={feature_bins.ndim}")
-        if len(feature_bins) < 2:
-            raise ValueError(f"All features must have at least two bin edges; len(bins[{i}])={len(feature_bins)}")
-        if not feature_bins.isfinite().all():
-            raise ValueError(f"Bin edges must not contain nan/inf/-inf; this is not true for feature {i}")
-        if (feature_bins[:-1] >= feature_bins[1:]).any():
-            raise ValueError(f"Bin edges must be sorted (strictly increasing); this is not true for feature {i}")
-        if len(feature_bins) == 2:
-            warnings.warn(
-                f"Feature {i} has just two bin edges, i.e. a single bin; its piecewise-linear encoding "
-                "is the same as min-max scaling"
-            )
 
 
 class LinearEmbeddings(nn.Module):
@@ -206,8 +185,6 @@ class CudaPiecewiseLinearEmbeddings(nn.Module):
             nn.init.zeros_(self.linear.weight)
         self.activation = nn.ReLU() if activation else None
 
-        n_bins_list = [int(e.numel() - 1) for e in bins]
-        max_n_bins = max(n_bins_list)
         base_device = bins[0].device
         for i, e in enumerate(bins):
             if e.device != base_device:
@@ -215,18 +192,11 @@ class CudaPiecewiseLinearEmbeddings(nn.Module):
                     "All bin tensors must be on the same device. "
                     f"bins[0].device={base_device}, bins[{i}].device={e.device}"
                 )
-        edges = torch.full((n_features, max_n_bins + 1), torch.inf, dtype=torch.float32, device=base_device)
-        inv_w = torch.zeros((n_features, max_n_bins), dtype=torch.float32, device=base_device)
-        for i, e in enumerate(bins):
-            e32 = e.to(device=base_device, dtype=torch.float32)
-            edges[i, : e32.numel()].copy_(e32)
-            inv_w[i, : e32.numel() - 1].copy_(torch.reciprocal(e32[1:] - e32[:-1]))
+        edges, inv_w, n_bins_t = bin_tables(bins, device=base_device)
         # non-persistent: the state_dict stays that of the upstream module
         self.register_buffer("_cuda_bin_edges", edges, persistent=False)
         self.register_buffer("_cuda_inv_bin_widths", inv_w, persistent=False)
-        self.register_buffer(
-            "_cuda_n_bins", torch.tensor(n_bins_list, dtype=torch.int32, device=base_device), persistent=False
-        )
+        self.register_buffer("_cuda_n_bins", n_bins_t, persistent=False)
 
     @property
     def n_features(self) -> int:

@@ -163,3 +163,63 @@ def test_module_errors_on_gpu():
         m(torch.zeros(4, 2, device="cuda"))
     with pytest.raises(ValueError):
         m(torch.zeros(4, 3, 1, device="cuda"))
+
+
+@pytest.mark.parametrize("version,activation", [("A", True), ("B", False), ("B", True)])
+def test_module_on_computed_bins(version, activation, c_oracle):
+    """compute_bins (quantile edges with duplicate collapse: discrete and
+    two-valued features give ragged and single-bin features) -> module on the
+    GPU, evaluated on the very samples the bins came from (so x sits exactly
+    on edges, the minimum and maximum included).  The forward is checked
+    against the CPU module; the gradients against the float64 closed form
+    with the fp32 ReLU decisions of the C mirror: at x == e_0 the dense CPU
+    formulation's addcmul rounding turns an exact 0 into +-1e-9, which a ReLU
+    then passes or blocks (upstream's rounding, "parity unpinned"), while the
+    reference kernel's arithmetic, like this one's, gives exactly 0."""
+    import numpy as np
+
+    from oracle import ple_oracle as po
+    from piecewiselinearembeddings_optimized_amd import bin_tables, compute_bins
+    from rtdl_num_embeddings_cuda import CudaPiecewiseLinearEmbeddings
+    from tests.ple_cases import FP32_ATOL, FP32_RTOL, close_scaled
+
+    rng = np.random.default_rng(17)
+    n = 4000
+    cols = [rng.standard_normal(n), rng.lognormal(0, 1, n), rng.poisson(3.0, n).astype(float),
+            np.where(rng.random(n) < 0.8, -1.0, 2.0), rng.uniform(-5, 5, n)]
+    X = torch.tensor(np.stack(cols, 1), dtype=torch.float32)
+    with pytest.warns(UserWarning):
+        bins = compute_bins(X, n_bins=32)
+    assert len({b.numel() for b in bins}) > 1 and min(b.numel() for b in bins) == 2
+    cpu = CudaPiecewiseLinearEmbeddings(bins, 16, activation=activation, version=version)
+    init_parameters_(cpu, seed=5)
+    if version == "B":
+        torch.nn.init.uniform_(cpu.linear.weight, -0.5, 0.5)
+    gpu = copy.deepcopy(cpu).to("cuda")
+    order = torch.argsort(X[:, 1])                     # includes feature 1's minimum and maximum
+    xb = torch.cat([X[order[:4]], X[order[-4:]], X[:120]])
+    xg = xb.cuda().requires_grad_(True)
+    og = gpu(xg)
+    with torch.no_grad():
+        oc = cpu(xb)
+    torch.testing.assert_close(og.detach().cpu(), oc, rtol=FORWARD_RTOL, atol=FORWARD_ATOL)
+    g = torch.randn(og.shape, generator=torch.Generator().manual_seed(6))
+    og.backward(g.cuda())
+
+    edges, iw, nb = (t.numpy() for t in bin_tables(bins))
+    w = cpu.linear.weight.detach().numpy()
+    bias = None if cpu.linear.bias is None else cpu.linear.bias.detach().numpy()
+    x_np = xb.numpy()
+    pre32, idx = c_oracle.forward_f32(x_np, edges, iw, nb, w, bias=bias)   # the kernel's fp32 pre-activation
+    lin = None if version == "A" else (cpu.linear0.weight.detach().numpy(), cpu.linear0.bias.detach().numpy())
+    ref = po.module_backward(g.numpy(), x_np, (edges, iw, nb), w, idx.astype(np.int64),
+                             pass_mask=po.relu_pass(pre32) if activation else None,
+                             has_bias=version == "A", linear0=lin)
+    got = {"dx": xg.grad, "dw": gpu.linear.weight.grad}
+    if version == "A":
+        got["db"] = gpu.linear.bias.grad
+    else:
+        got["dlw"], got["dlb"] = gpu.linear0.weight.grad, gpu.linear0.bias.grad
+    for key, t in got.items():
+        ok, worst = close_scaled(t.cpu().numpy(), ref[key], ref[key + "_abs"], FP32_RTOL, FP32_ATOL)
+        assert ok, (key, worst)
