@@ -14,7 +14,8 @@ reference kernel for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters to
 bytes).  ``--mode module`` times the whole module in the reference
 benchmark's configuration (version B, no activation; forward and
 forward+backward), fused against the reference's op sequence (the forward
-operator followed by PyTorch's linear0 and residual add).
+operator followed by PyTorch's linear0 and residual add).  ``--mode encode``
+times the dense encoding kernels (``encode`` / ``encode_backward``).
 
 Timing follows the reference harness's discipline (warm-up, then timed
 repetitions between device events on the stream the kernels run on).  The
@@ -42,7 +43,7 @@ def _parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=1)
-    ap.add_argument("--mode", choices=("fwdbwd", "fwd", "module", "copy"), default="fwdbwd")
+    ap.add_argument("--mode", choices=("fwdbwd", "fwd", "module", "encode", "copy"), default="fwdbwd")
     ap.add_argument("--version", choices=("A", "B"), default="B", help="module version (--mode module)")
     ap.add_argument("--activation", action="store_true", help="ReLU in the module (--mode module)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -179,6 +180,52 @@ def _module_bench(args):
     print(json.dumps(line), flush=True)
 
 
+def _encode_bench(args):
+    """Dense encoding output [N, sum n_f] and its dx, with HBM bytes per launch."""
+    import numpy as np
+    import torch
+
+    import piecewiselinearembeddings_optimized_amd  # noqa: F401
+    from piecewiselinearembeddings_optimized_amd import workloads
+
+    dev = torch.device("cuda:0")
+    ops = torch.ops.rtdl_num_embeddings_cuda
+    w = workloads.make(args.config)
+    n, f, bmax, d = w.shape
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    nbins = w.n_bins.astype(np.int64)
+    offs = np.concatenate([[0], np.cumsum(nbins)[:-1]]).astype(np.int32)
+    total = int(nbins.sum())
+    x, e, iw, nb, of = t(w.x), t(w.edges), t(w.inv_widths), t(w.n_bins), t(offs)
+    g = torch.randn((n, total), device=dev, generator=torch.Generator(dev).manual_seed(0))
+
+    def tm(fn):
+        for _ in range(max(args.warmup, 1)):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(args.steps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / args.steps
+
+    fwd_ms = tm(lambda: ops.encode(x, e, iw, nb, of, total))
+    bwd_ms = tm(lambda: ops.encode_backward(g, x, e, iw, nb, of))
+    fwd_bytes = n * total * 4 + n * f * 4                    # output + x
+    bwd_bytes = n * f * (4 + 4) + n * f * 128                # x, dx, and one 128-byte line of g per pair
+    print(json.dumps({
+        "metric": f"dense encoding samples/s ({w.name}, {total} columns)", "value": n / (fwd_ms * 1e-3),
+        "unit": "samples/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": fwd_ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": w.name, "N": n, "F": f, "total_bins": total, "mode": "encode"},
+        "fwd_ms": fwd_ms, "fwd_GBps": fwd_bytes / (fwd_ms * 1e-3) / 1e9,
+        "fwd_frac": fwd_bytes / (fwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "bwd_ms": bwd_ms, "bwd_GBps_line_bound": bwd_bytes / (bwd_ms * 1e-3) / 1e9,
+    }), flush=True)
+
+
 def main():
     args = _parse()
     if args.mode == "copy":
@@ -186,6 +233,9 @@ def main():
         return
     if args.mode == "module":
         _module_bench(args)
+        return
+    if args.mode == "encode":
+        _encode_bench(args)
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -15,6 +15,10 @@
  *                           (registered at csrc/ops.cpp:35-44, :62-75)
  *   ple_backward_launch  <- ple_backward_cuda  csrc/backward_cuda.cu:1528-1725
  *                           (registered at csrc/ops.cpp:46-58, :62-75)
+ *   ple_encode_launch / ple_encode_backward_launch
+ *                        <- upstream rtdl_num_embeddings.PiecewiseLinearEncoding
+ *                           (external dependency of the reference, pinned at
+ *                           requirements.txt:1; no operator counterpart)
  *   ple_forward_epilogue_launch / ple_backward_epilogue_launch
  *                        <- the module tail run as PyTorch ops after the
  *                           forward operator, src/rtdl_num_embeddings_cuda/
@@ -166,6 +170,28 @@ int ple_backward_epilogue_launch(const float *grad_output, const float *x, const
                                  float *grad_bias, float *grad_lin_weight, float *grad_lin_bias,
                                  int64_t N, int64_t F, int64_t B, int64_t D, int quant_dtype,
                                  void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Dense piecewise-linear encoding: the output of the upstream
+ * PiecewiseLinearEncoding module (rtdl_num_embeddings==0.0.12), which the
+ * reference's module builds on; no counterpart in the reference's operators.
+ * For feature f (n_bins[f] = n bins, b and frac as in ple_forward_launch) the
+ * n components at columns offsets[f] .. offsets[f] + n - 1 of row n are
+ *   1 (k < b), frac (k == b), 0 (k > b);   NaN x: all NaN.
+ *   offsets         int32 [F], offsets[f] = sum_{j<f} n_bins[j]
+ *   output          float32 [N, total_bins], total_bins = sum_f n_bins[f]
+ * F * 8 * 8 + 4 bytes of per-feature tables must fit LDS (F <= 2500).
+ */
+int ple_encode_launch(const float *x, const float *bin_edges, const float *inv_bin_widths,
+                      const int32_t *n_bins, const int32_t *offsets, float *output, int64_t N,
+                      int64_t F, int64_t B, int64_t total_bins, void *stream);
+
+/* Backward of ple_encode_launch: grad_x[n, f] = g[n, offsets[f] + b] * iw_b
+ * (+ g[n, offsets[f] + b - 1] * iw_{b-1} when b > 0 and x == e_b). */
+int ple_encode_backward_launch(const float *grad_output, const float *x, const float *bin_edges,
+                               const float *inv_bin_widths, const int32_t *n_bins,
+                               const int32_t *offsets, float *grad_x, int64_t N, int64_t F,
+                               int64_t B, int64_t total_bins, void *stream);
 
 /* Human-readable name of a return code (static storage). */
 const char *ple_error_string(int code);

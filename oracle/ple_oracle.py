@@ -458,3 +458,63 @@ def module_backward(grad_output, x, bins_tables, weight, idx, pass_mask=None, ha
     r["dlw"], r["dlw_abs"] = gx.sum(0), np.abs(gx).sum(0)
     r["dlb"], r["dlb_abs"] = g.sum(0), np.abs(g).sum(0)
     return r
+
+
+# ----------------------------------------------------------------------------
+# dense encoding output (upstream PiecewiseLinearEncoding), closed form
+# ----------------------------------------------------------------------------
+
+
+def encoding_offsets(n_bins) -> np.ndarray:
+    nb = np.asarray(n_bins, dtype=np.int64)
+    return np.concatenate([[0], np.cumsum(nb)[:-1]]).astype(np.int64)
+
+
+def encoding_closed_form(x, bin_edges, inv_bin_widths, n_bins, dtype=np.float64):
+    """``[N, sum n_f]``: per feature ``1`` below the active bin, ``frac`` at it,
+    ``0`` above; NaN x gives NaN components.  ``dtype=np.float32`` evaluates
+    ``frac = (x - e_b) * iw_b`` with two fp32 roundings, the kernel's
+    arithmetic; float64 gives the exact value of the same expression."""
+    x = np.asarray(x, dtype=np.float32)
+    n, f_count = x.shape
+    idx = bin_indices(x, bin_edges, n_bins)
+    f_idx = np.arange(f_count)[None, :]
+    with np.errstate(invalid="ignore", over="ignore"):
+        if dtype == np.float32:
+            frac = (x - bin_edges[f_idx, idx]).astype(np.float32) * inv_bin_widths[f_idx, idx]
+        else:
+            frac = (x.astype(np.float64) - bin_edges[f_idx, idx].astype(np.float64)) * \
+                inv_bin_widths[f_idx, idx].astype(np.float64)
+    offs = encoding_offsets(n_bins)
+    total = int(np.sum(n_bins))
+    out = np.zeros((n, total), dtype=dtype)
+    for f in range(f_count):
+        nf = int(n_bins[f])
+        k = np.arange(nf)[None, :]
+        b = idx[:, f:f + 1]
+        val = np.where(k < b, 1.0, np.where(k == b, frac[:, f:f + 1], 0.0))
+        val = np.where(np.isnan(x[:, f:f + 1]), np.nan, val)
+        out[:, offs[f]:offs[f] + nf] = val
+    return out
+
+
+def encoding_backward(grad_output, x, bin_edges, inv_bin_widths, n_bins):
+    """``dx[n, f] = g[off_f + b] iw_b (+ g[off_f + b - 1] iw_{b-1} if b > 0 and
+    x == e_b)`` in float64, with the sum of |terms|."""
+    g = np.asarray(grad_output, dtype=np.float64)
+    x = np.asarray(x, dtype=np.float32)
+    n, f_count = x.shape
+    idx = bin_indices(x, bin_edges, n_bins)
+    offs = encoding_offsets(n_bins)
+    rows = np.arange(n)
+    dx = np.zeros((n, f_count))
+    dx_abs = np.zeros((n, f_count))
+    for f in range(f_count):
+        b = idx[:, f]
+        t = g[rows, offs[f] + b] * inv_bin_widths[f, b].astype(np.float64)
+        edge = (b > 0) & (x[:, f] == bin_edges[f, b])
+        bm = np.maximum(b - 1, 0)
+        t2 = np.where(edge, g[rows, offs[f] + bm] * inv_bin_widths[f, bm].astype(np.float64), 0.0)
+        dx[:, f] = t + t2
+        dx_abs[:, f] = np.abs(t) + np.abs(t2)
+    return dx, dx_abs

@@ -16,11 +16,12 @@ import torch  # noqa: F401  (loads the HIP runtime the extension links against)
 from . import _C as _C  # noqa: F401
 from . import _meta as _meta  # noqa: F401
 from . import _autograd as _autograd  # noqa: F401
-from .module import CudaPiecewiseLinearEmbeddings
+from .module import CudaPiecewiseLinearEmbeddings, CudaPiecewiseLinearEncoding
 from .bins import bin_tables, compute_bins
 
 __all__ = [
     "CudaPiecewiseLinearEmbeddings",
+    "CudaPiecewiseLinearEncoding",
     "bin_tables",
     "compute_bins",
 ]

@@ -14,6 +14,8 @@ did.
 ``lin_weight`` (6) and ``lin_bias`` (7) from one backward launch, which reads
 the forward's ReLU pass bits (saved, non-differentiable).
 
+``encode``: the gradient of ``x`` (input 0) from ``encode_backward``.
+
 Double backward is not implemented (as in the reference).
 """
 
@@ -122,4 +124,25 @@ torch.library.register_autograd(
     "rtdl_num_embeddings_cuda::forward_epilogue",
     _forward_epilogue_backward,
     setup_context=_setup_forward_epilogue_context,
+)
+
+
+def _setup_encode_context(ctx: Any, inputs, output) -> None:
+    x, bin_edges, inv_bin_widths, n_bins, offsets, _total = inputs
+    ctx.save_for_backward(x, bin_edges, inv_bin_widths, n_bins, offsets)
+    ctx.set_materialize_grads(False)
+
+
+def _encode_backward(ctx: Any, grad_output):
+    if grad_output is None or not ctx.needs_input_grad[0]:
+        return (None,) * 6
+    x, bin_edges, inv_bin_widths, n_bins, offsets = ctx.saved_tensors
+    gx = _ops.encode_backward(grad_output.contiguous(), x, bin_edges, inv_bin_widths, n_bins, offsets)
+    return gx, None, None, None, None, None
+
+
+torch.library.register_autograd(
+    "rtdl_num_embeddings_cuda::encode",
+    _encode_backward,
+    setup_context=_setup_encode_context,
 )

@@ -158,3 +158,19 @@ def _backward_epilogue_fake(grad_output, x, bin_edges, inv_bin_widths, n_bins, w
 
     return (_maybe(x, x, compute_grad_x), _maybe(weight, weight, compute_grad_weight), fd(compute_grad_bias),
             fd(compute_grad_lin_weight), fd(compute_grad_lin_bias))
+
+
+@torch.library.register_fake("rtdl_num_embeddings_cuda::encode")
+def _encode_fake(x, bin_edges, inv_bin_widths, n_bins, offsets, total_bins):
+    torch._check(x.ndim == 2 and x.dtype == torch.float32, lambda: "x must be float32 [N, F]")
+    torch._check(n_bins.shape[0] == x.shape[1], lambda: "n_bins must be int32 [F]")
+    torch._check(offsets.shape[0] == x.shape[1], lambda: "offsets must be int32 [F]")
+    torch._check(total_bins > 0, lambda: "total_bins must be positive")
+    return torch.empty((x.shape[0], total_bins), dtype=torch.float32, device=x.device)
+
+
+@torch.library.register_fake("rtdl_num_embeddings_cuda::encode_backward")
+def _encode_backward_fake(grad_output, x, bin_edges, inv_bin_widths, n_bins, offsets):
+    torch._check(grad_output.ndim == 2 and grad_output.shape[0] == x.shape[0],
+                 lambda: "grad_output must be contiguous float32 [N, total_bins]")
+    return torch.empty_like(x)

@@ -66,6 +66,10 @@ def lib() -> ctypes.CDLL:
         L.ple_backward_epilogue_launch.argtypes = [p, p, p, p, p, p, p, ep, p, p, p, p, p, i64, i64, i64, i64, i32,
                                                    p, sz, p]
         L.ple_backward_epilogue_launch.restype = i32
+        L.ple_encode_launch.argtypes = [p, p, p, p, p, p, i64, i64, i64, i64, p]
+        L.ple_encode_launch.restype = i32
+        L.ple_encode_backward_launch.argtypes = [p, p, p, p, p, p, p, i64, i64, i64, i64, p]
+        L.ple_encode_backward_launch.restype = i32
         _lib = L
     return _lib
 
@@ -151,3 +155,19 @@ def backward_epilogue(grad_output, x, bin_edges, inv_bin_widths, n_bins, weight,
         _ptr(bin_indices), ctypes.byref(epi), _ptr(grad_x), _ptr(grad_weight), _ptr(grad_bias),
         _ptr(grad_lin_weight), _ptr(grad_lin_bias), n, f, bmax, d, dtype_code(quant_dtype), _ptr(workspace),
         ws_bytes, _stream(stream)))
+
+
+def encode(x, bin_edges, inv_bin_widths, n_bins, offsets, output, stream=None) -> None:
+    """``ple_encode_launch`` into a caller-provided fp32 ``output`` [N, total_bins]."""
+    n, f = x.shape
+    check(lib().ple_encode_launch(
+        _ptr(x), _ptr(bin_edges), _ptr(inv_bin_widths), _ptr(n_bins), _ptr(offsets), _ptr(output), n, f,
+        inv_bin_widths.shape[1], output.shape[1], _stream(stream)))
+
+
+def encode_backward(grad_output, x, bin_edges, inv_bin_widths, n_bins, offsets, grad_x, stream=None) -> None:
+    """``ple_encode_backward_launch`` into a caller-provided fp32 ``grad_x`` [N, F]."""
+    n, f = x.shape
+    check(lib().ple_encode_backward_launch(
+        _ptr(grad_output), _ptr(x), _ptr(bin_edges), _ptr(inv_bin_widths), _ptr(n_bins), _ptr(offsets),
+        _ptr(grad_x), n, f, inv_bin_widths.shape[1], grad_output.shape[1], _stream(stream)))

@@ -172,4 +172,40 @@ int ple_backward_epilogue_launch(const float *grad_output, const float *x, const
     return ple::backward_run(r);
 }
 
+int ple_encode_launch(const float *x, const float *bin_edges, const float *inv_bin_widths,
+                      const int32_t *n_bins, const int32_t *offsets, float *output, int64_t N,
+                      int64_t F, int64_t B, int64_t total_bins, void *stream) {
+    const int rc = ple::check_common(N, F, B, 1);
+    if (rc != PLE_OK) return rc;
+    if (total_bins < 1) return PLE_E_BAD_SHAPE;
+    if (N == 0) return PLE_OK;
+    if (N > INT64_MAX / total_bins) return PLE_E_TOO_LARGE;
+    if (!x || !bin_edges || !inv_bin_widths || !n_bins || !offsets || !output) return PLE_E_NULL_POINTER;
+    ple::EncodeRequest r;
+    r.x = x; r.edges = bin_edges; r.iw = inv_bin_widths; r.nbins = n_bins; r.offsets = offsets;
+    r.out = output;
+    r.N = N; r.F = F; r.B = B; r.T = total_bins;
+    r.stream = static_cast<hipStream_t>(stream);
+    return ple::encode_run(r);
+}
+
+int ple_encode_backward_launch(const float *grad_output, const float *x, const float *bin_edges,
+                               const float *inv_bin_widths, const int32_t *n_bins,
+                               const int32_t *offsets, float *grad_x, int64_t N, int64_t F,
+                               int64_t B, int64_t total_bins, void *stream) {
+    const int rc = ple::check_common(N, F, B, 1);
+    if (rc != PLE_OK) return rc;
+    if (total_bins < 1) return PLE_E_BAD_SHAPE;
+    if (N == 0) return PLE_OK;
+    if (N > INT64_MAX / total_bins) return PLE_E_TOO_LARGE;
+    if (!grad_output || !x || !bin_edges || !inv_bin_widths || !n_bins || !offsets || !grad_x)
+        return PLE_E_NULL_POINTER;
+    ple::EncodeRequest r;
+    r.g = grad_output; r.x = x; r.edges = bin_edges; r.iw = inv_bin_widths; r.nbins = n_bins;
+    r.offsets = offsets; r.out = grad_x;
+    r.N = N; r.F = F; r.B = B; r.T = total_bins;
+    r.stream = static_cast<hipStream_t>(stream);
+    return ple::encode_backward_run(r);
+}
+
 }  // extern "C"

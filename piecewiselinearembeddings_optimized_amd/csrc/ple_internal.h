@@ -57,4 +57,16 @@ struct BackwardRequest {
 size_t backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D);
 int backward_run(const BackwardRequest &r);
 
+struct EncodeRequest {
+    const float *x, *edges, *iw;
+    const int32_t *nbins, *offsets;
+    const float *g = nullptr;    // backward: grad_output [N, T]
+    float *out;                  // forward: encoding [N, T]; backward: grad_x [N, F]
+    int64_t N, F, B, T;
+    hipStream_t stream;
+};
+
+int encode_run(const EncodeRequest &r);
+int encode_backward_run(const EncodeRequest &r);
+
 }  // namespace ple

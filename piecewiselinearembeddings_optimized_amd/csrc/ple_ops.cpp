@@ -375,6 +375,60 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> ple_backw
     return {grad_x, grad_weight, grad_bias, grad_lw, grad_lb};
 }
 
+void check_encode_tables(const at::Tensor &x, const at::Tensor &bin_edges, const at::Tensor &inv_bin_widths,
+                         const at::Tensor &n_bins, const at::Tensor &offsets) {
+    for (const at::Tensor *t : {&x, &bin_edges, &inv_bin_widths, &n_bins, &offsets}) {
+        TORCH_CHECK(t->is_cuda() && t->device() == x.device(), "All encoding tensors must be on the same CUDA device");
+        TORCH_CHECK(t->is_contiguous(), "encoding tensors must be contiguous");
+    }
+    TORCH_CHECK(x.dim() == 2 && x.scalar_type() == at::kFloat, "x must be float32 [N, F]");
+    const int64_t F = x.size(1);
+    TORCH_CHECK(bin_edges.dim() == 2 && bin_edges.size(0) == F && bin_edges.scalar_type() == at::kFloat,
+                "bin_edges must be float32 [F, B + 1]");
+    TORCH_CHECK(inv_bin_widths.dim() == 2 && inv_bin_widths.size(0) == F &&
+                    inv_bin_widths.size(1) + 1 == bin_edges.size(1) && inv_bin_widths.scalar_type() == at::kFloat,
+                "inv_bin_widths must be float32 [F, B]");
+    TORCH_CHECK(n_bins.dim() == 1 && n_bins.size(0) == F && n_bins.scalar_type() == at::kInt, "n_bins must be int32 [F]");
+    TORCH_CHECK(offsets.dim() == 1 && offsets.size(0) == F && offsets.scalar_type() == at::kInt,
+                "offsets must be int32 [F]");
+}
+
+// The upstream PiecewiseLinearEncoding output (this build's addition).
+at::Tensor ple_encode(const at::Tensor &x, const at::Tensor &bin_edges, const at::Tensor &inv_bin_widths,
+                      const at::Tensor &n_bins, const at::Tensor &offsets, int64_t total_bins) {
+    check_encode_tables(x, bin_edges, inv_bin_widths, n_bins, offsets);
+    TORCH_CHECK(total_bins > 0, "total_bins must be positive");
+    const int64_t N = x.size(0), F = x.size(1), B = inv_bin_widths.size(1);
+    DeviceScope scope(x.device().index());
+    at::Tensor out = at::empty({N, total_bins}, x.options());
+    if (N == 0) return out;
+    const int rc = ple_encode_launch(x.data_ptr<float>(), bin_edges.data_ptr<float>(), inv_bin_widths.data_ptr<float>(),
+                                     n_bins.data_ptr<int32_t>(), offsets.data_ptr<int32_t>(), out.data_ptr<float>(), N,
+                                     F, B, total_bins, current_stream(x));
+    check_rc(rc, "ple_encode_launch");
+    return out;
+}
+
+at::Tensor ple_encode_backward(const at::Tensor &grad_output, const at::Tensor &x, const at::Tensor &bin_edges,
+                               const at::Tensor &inv_bin_widths, const at::Tensor &n_bins,
+                               const at::Tensor &offsets) {
+    check_encode_tables(x, bin_edges, inv_bin_widths, n_bins, offsets);
+    TORCH_CHECK(grad_output.is_cuda() && grad_output.device() == x.device() && grad_output.is_contiguous() &&
+                    grad_output.scalar_type() == at::kFloat && grad_output.dim() == 2 &&
+                    grad_output.size(0) == x.size(0),
+                "grad_output must be contiguous float32 [N, total_bins]");
+    const int64_t N = x.size(0), F = x.size(1), B = inv_bin_widths.size(1), T = grad_output.size(1);
+    DeviceScope scope(x.device().index());
+    at::Tensor grad_x = at::empty_like(x);
+    if (N == 0) return grad_x;
+    const int rc = ple_encode_backward_launch(
+        grad_output.data_ptr<float>(), x.data_ptr<float>(), bin_edges.data_ptr<float>(),
+        inv_bin_widths.data_ptr<float>(), n_bins.data_ptr<int32_t>(), offsets.data_ptr<int32_t>(),
+        grad_x.data_ptr<float>(), N, F, B, T, current_stream(x));
+    check_rc(rc, "ple_encode_backward_launch");
+    return grad_x;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(rtdl_num_embeddings_cuda, m) {
@@ -403,6 +457,12 @@ TORCH_LIBRARY(rtdl_num_embeddings_cuda, m) {
         "ScalarType quant_dtype, bool compute_grad_x, bool compute_grad_weight, bool compute_grad_bias, "
         "bool compute_grad_lin_weight, bool compute_grad_lin_bias) -> (Tensor grad_x, Tensor grad_weight, "
         "Tensor grad_bias, Tensor grad_lin_weight, Tensor grad_lin_bias)");
+    m.def(
+        "encode(Tensor x, Tensor bin_edges, Tensor inv_bin_widths, Tensor n_bins, Tensor offsets, int total_bins) "
+        "-> Tensor");
+    m.def(
+        "encode_backward(Tensor grad_output, Tensor x, Tensor bin_edges, Tensor inv_bin_widths, Tensor n_bins, "
+        "Tensor offsets) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(rtdl_num_embeddings_cuda, CUDA, m) {
@@ -412,6 +472,8 @@ TORCH_LIBRARY_IMPL(rtdl_num_embeddings_cuda, CUDA, m) {
     m.impl("backward_with_bias", &ple_backward_with_bias);
     m.impl("forward_epilogue", &ple_forward_epilogue);
     m.impl("backward_epilogue", &ple_backward_epilogue);
+    m.impl("encode", &ple_encode);
+    m.impl("encode_backward", &ple_encode_backward);
 }
 
 // Importing the extension module runs the registrations above; the module

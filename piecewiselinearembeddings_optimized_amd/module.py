@@ -141,6 +141,57 @@ class PiecewiseLinearEncodingBuffers(nn.Module):
         return x
 
 
+class CudaPiecewiseLinearEncoding(nn.Module):
+    """Dense piecewise-linear encoding (upstream ``PiecewiseLinearEncoding``).
+
+    Output ``[batch, total_n_bins]``, ``total_n_bins = sum_f n_f``: per feature
+    its ``n_f`` components in bin order (the phantom slots of the padded layout
+    dropped, as upstream's mask does).  On a HIP device the encoding and the
+    gradient of ``x`` run in the ``encode`` / ``encode_backward`` kernels; on
+    the CPU the upstream dense computation runs.  No parameters.
+    """
+
+    def __init__(self, bins: list[Tensor]) -> None:
+        check_bins(bins)
+        super().__init__()
+        self.impl = PiecewiseLinearEncodingBuffers(bins)
+        base_device = bins[0].device
+        for i, e in enumerate(bins):
+            if e.device != base_device:
+                raise ValueError(
+                    "All bin tensors must be on the same device. "
+                    f"bins[0].device={base_device}, bins[{i}].device={e.device}"
+                )
+        edges, inv_w, n_bins = bin_tables(bins, device=base_device)
+        offsets = torch.zeros_like(n_bins)
+        offsets[1:] = torch.cumsum(n_bins, 0)[:-1]
+        self.register_buffer("_cuda_bin_edges", edges, persistent=False)
+        self.register_buffer("_cuda_inv_bin_widths", inv_w, persistent=False)
+        self.register_buffer("_cuda_n_bins", n_bins, persistent=False)
+        self.register_buffer("_cuda_offsets", offsets.to(torch.int32), persistent=False)
+        self._total_n_bins = int(sum(int(e.numel()) - 1 for e in bins))
+
+    def get_output_shape(self) -> torch.Size:
+        return torch.Size((self._total_n_bins,))
+
+    def forward(self, x: Tensor) -> Tensor:
+        if x.ndim != 2:
+            raise ValueError("Only inputs with shape [batch_size, n_features] are supported")
+        if x.shape[1] != self._cuda_n_bins.shape[0]:
+            raise ValueError(f"Expected {self._cuda_n_bins.shape[0]} numerical features, got {x.shape[1]}")
+        if x.device.type != "cuda":
+            enc = self.impl(x)
+            return enc.flatten(-2) if self.impl.mask is None else enc[:, self.impl.mask]
+        if x.device != self._cuda_bin_edges.device:
+            raise RuntimeError("x and the module must be on the same CUDA device")
+        if x.dtype != torch.float32:
+            raise TypeError(f"The fused CUDA path requires float32 x. Got {x.dtype}.")
+        if not x.is_contiguous():
+            raise ValueError("The fused CUDA path requires contiguous x.")
+        return _ops.encode(x, self._cuda_bin_edges, self._cuda_inv_bin_widths, self._cuda_n_bins,
+                           self._cuda_offsets, self._total_n_bins)
+
+
 class CudaPiecewiseLinearEmbeddings(nn.Module):
     """Piecewise-linear embeddings with the PLE branch fused on HIP devices.
 

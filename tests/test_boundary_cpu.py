@@ -223,3 +223,26 @@ def test_module_rejects_bad_shapes_on_cpu():
         m(torch.zeros(4, 3, 1))
     with pytest.raises(ValueError):
         m(torch.zeros(4, 2))
+
+
+@pytest.mark.parametrize("case_name", ["equal", "ragged", "single_bin", "all_single_bin"])
+def test_encoding_module_cpu_path_is_the_upstream_dense_encoding(case_name):
+    import numpy as np
+
+    from oracle import ple_oracle as po
+    from piecewiselinearembeddings_optimized_amd import CudaPiecewiseLinearEncoding
+    from tests.ple_cases import make_bins, sample_features
+
+    bins = make_bins(case_name)
+    m = CudaPiecewiseLinearEncoding(bins)
+    total = sum(len(b) - 1 for b in bins)
+    assert m.get_output_shape() == torch.Size((total,))
+    assert list(m.state_dict()) == [k for k in ("impl.weight", "impl.bias", "impl.single_bin_mask", "impl.mask")
+                                   if getattr(m.impl, k.split(".")[1]) is not None]
+    x = sample_features(bins, batch_size=64, seed=3)
+    out = m(x)
+    assert out.shape == (64, total) and out.dtype == torch.float32
+    edges, iw, nb = po.pad_bins([b.numpy() for b in bins])
+    np.testing.assert_allclose(out.numpy(), po.encoding_closed_form(x.numpy(), edges, iw, nb), rtol=1e-5, atol=1e-5)
+    with pytest.raises(ValueError):
+        m(x[:, :1])

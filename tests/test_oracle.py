@@ -404,3 +404,53 @@ def test_pass_bits_pack_and_unpack():
         j = d - 1
         np.testing.assert_array_equal((words.view(np.uint32)[..., j // 32] >> (j % 32)) & 1, passm[..., j])
     assert po.relu_pass(np.array([np.nan, -0.0, 0.0, 1e-30, -1e-30])).tolist() == [True, False, False, True, False]
+
+
+# ---------------------------------------------------------------------------
+# dense encoding output: closed form vs the upstream dense formulation
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case_name", BIN_CASE_NAMES)
+def test_encoding_closed_form_equals_dense(case_name):
+    bins, x, edges, iw, nb, w, b, g = _case(case_name, 4, 41)
+    enc, passm, width = po.dense_encoding(x, bins)
+    real = ~np.isnan(width)                                  # [F, Bmax] real slots, in slot order
+    dense = np.concatenate([enc[:, f, real[f]] for f in range(len(bins))], axis=1)
+    closed = po.encoding_closed_form(x, edges, iw, nb)
+    assert closed.shape == (x.shape[0], int(nb.sum()))
+    np.testing.assert_allclose(closed, dense, rtol=1e-6, atol=1e-6)
+    # the fp32 evaluation differs from the float64 one by the two roundings only
+    c32 = po.encoding_closed_form(x, edges, iw, nb, dtype=np.float32)
+    np.testing.assert_allclose(c32, closed, rtol=3e-7, atol=1e-7)
+
+
+@pytest.mark.parametrize("case_name", BIN_CASE_NAMES)
+def test_encoding_backward_equals_torch_autograd_of_dense(case_name):
+    bins, x, edges, iw, nb, w, b, _ = _case(case_name, 4, 43)
+    total = int(nb.sum())
+    g = np.random.default_rng(7).standard_normal((x.shape[0], total))
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    eye = np.zeros((len(bins), edges.shape[1] - 1, total))
+    offs = po.encoding_offsets(nb)
+    _, width, _ = po.dense_layout(bins)
+    for f in range(len(bins)):
+        slots = np.flatnonzero(~np.isnan(width[f]))
+        eye[f, slots, offs[f] + np.arange(len(slots))] = 1.0
+    # the dense encoding, then a fixed 0/1 map that drops phantom slots and flattens
+    left, width_t, single = po.dense_layout(bins)
+    lt = torch.tensor(np.nan_to_num(left))
+    wt = torch.tensor(np.nan_to_num(width_t, nan=1.0))
+    raw = (xt[:, :, None] - lt[None]) / wt[None]
+    bmax = left.shape[1]
+    if bmax > 1:
+        first = raw[..., :1].clamp_max(1.0)
+        mid = raw[..., 1:-1].clamp(0.0, 1.0)
+        last = raw[..., -1:]
+        last = torch.where(torch.tensor(single)[None, :, None], last, last.clamp_min(0.0))
+        enc = torch.cat([first, mid, last], dim=-1)
+    else:
+        enc = raw
+    flat = torch.einsum("nfb,fbt->nt", enc, torch.tensor(eye))
+    flat.backward(torch.tensor(g))
+    dx, _ = po.encoding_backward(g, x, edges, iw, nb)
+    np.testing.assert_allclose(dx, xt.grad.numpy(), rtol=2e-6, atol=2e-6)
