@@ -171,26 +171,26 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_sort_kernel(BwdArgs a) {
 
     // pair inputs: thread -> pairs i = tid + u * kBlock, i -> (sample i / FS,
     // feature i % FS); unconditional loads (pair 0 stands in for padding)
+    // FS and NT are powers of two: shifts instead of integer divisions
+    const int fs_shift = __ffs(FS) - 1;
+    const int nt_shift = __ffs(NT) - 1;
     int pk[kPairsPerThread];
     float pv[kPairsPerThread];
 #pragma unroll
     for (int u = 0; u < kPairsPerThread; ++u) {
         const int i = tid + u * kBlock;
-        const int s = i / FS;
-        const int fl = i - s * FS;
+        const int s = i >> fs_shift;
+        const int fl = i & (FS - 1);
         const int64_t pair = (s < ns && fl < nfh) ? (sub + s) * F + f0 + fl : 0;
         pk[u] = load_idx<IdxT>(a.idx, pair);
         pv[u] = a.x[pair];
     }
     for (int i = tid; i < FS; i += kBlock) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
-    for (int i = tid; i < FS * KB; i += kBlock) {
-        const int fl = i / KB;
-        s_edge[i] = fl < nfh ? a.edges[static_cast<int64_t>(f0) * KB + i] : 0.0f;
-    }
-    for (int i = tid; i < FS * B; i += kBlock) {
-        const int fl = i / B;
-        s_iw[i] = fl < nfh ? a.iw[static_cast<int64_t>(f0) * B + i] : 0.0f;
-    }
+    // (rows past the last feature are never read: their pairs are padding)
+    for (int i = tid; i < FS * KB; i += kBlock)
+        s_edge[i] = i < nfh * KB ? a.edges[static_cast<int64_t>(f0) * KB + i] : 0.0f;
+    for (int i = tid; i < FS * B; i += kBlock)
+        s_iw[i] = i < nfh * B ? a.iw[static_cast<int64_t>(f0) * B + i] : 0.0f;
     for (int i = tid; i < NB * KB; i += kBlock) s_cnt[i] = 0;
     __syncthreads();
 
@@ -198,8 +198,8 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_sort_kernel(BwdArgs a) {
 #pragma unroll
     for (int u = 0; u < kPairsPerThread; ++u) {
         const int i = tid + u * kBlock;
-        const int s = i / FS;
-        const int fl = i - s * FS;
+        const int s = i >> fs_shift;
+        const int fl = i & (FS - 1);
         int key = B;
         float qf = 0.0f;
         if (s < ns && fl < nfh) {
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_sort_kernel(BwdArgs a) {
             qf = quant<Q>((v - e) * s_iw[fl * B + k]);
             key = k | ((k > 0 && v == e) ? 0x8000 : 0);
         }
-        s_info[fl * NT + s] = make_float2(qf, __int_as_float(key));
+        s_info[(fl << nt_shift) + s] = make_float2(qf, __int_as_float(key));
     }
     __syncthreads();
 
@@ -233,7 +233,9 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_sort_kernel(BwdArgs a) {
     // C. per key: exclusive prefix of its counts over the feature's blocks
     //    (held in registers), then {count | pieces << 16} for the scan
     for (int kk = tid; kk < FS * KB; kk += kBlock) {
-        const int fl = kk / KB;
+        // fl = kk / KB without a division (FS <= 16)
+        int fl = 0;
+        while (fl + 1 < FS && kk >= (fl + 1) * KB) ++fl;
         const int k = kk - fl * KB;
         uint16_t *col = s_cnt + fl * NBf * KB + k;
         int cc[kMaxBlocksPerFeature];
@@ -256,8 +258,8 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_sort_kernel(BwdArgs a) {
     // D. scatter: sorted position -> row descriptor; the first row of every
     //    piece writes the piece's entry
     for (int p = tid; p < kP; p += kBlock) {
-        const int fl = p / NT;
-        const int s = p - fl * NT;
+        const int fl = p >> nt_shift;
+        const int s = p & (NT - 1);
         const float2 inf = s_info[p];
         const int kb = __float_as_int(inf.y);
         const int k = kb & 0x7fff;
@@ -650,8 +652,8 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
 #pragma unroll
             for (int u = 0; u < kPairsPerThread; ++u) {
                 const int p = tid + u * kBlock;
-                const int fl = p / NT;
-                const int sidx = p - fl * NT;
+                const int fl = p >> nt_shift;
+                const int sidx = p & (NT - 1);
                 if (fl < nfh && sidx < ns) a.dxt[static_cast<int64_t>(f0 + fl) * a.N + sub + sidx] = s_dx[s_inv[p]];
             }
         }
