@@ -291,8 +291,9 @@ __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
 
 // LDS per workgroup the planner aims for: small tables keep many workgroups
 // (and their loads) in flight per CU, which the store stream needs more than
-// wide feature groups.
-constexpr size_t kLdsBudget = 24 * 1024;
+// wide feature groups.  (Measured at F=128, 48 bins, d=32: two features per
+// workgroup, 25 KB, beat one by 3-11 us; four, 50 KB, lost 15-40 us.)
+constexpr size_t kLdsBudget = 32 * 1024;
 
 int env_int(const char *name, int dflt) {
     const char *s = getenv(name);
