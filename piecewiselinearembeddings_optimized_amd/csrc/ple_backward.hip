@@ -586,6 +586,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
                     iwp = s_iw[rowbase + kp];
                 }
                 const int rs = static_cast<int>((pe >> 16) & 0xfff);
+                float parts[kL];
 #pragma unroll
                 for (int i = 0; i < kL; ++i) {
                     const float qf = __uint_as_float(dsc[i].x);
@@ -613,12 +614,24 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
                     float part = dot * iwk;
                     if constexpr (kLin) part += dotl;
                     // x on the bin's left edge (k >= 1): the lower bin's term too
-                    part = dsc[i].x == 0x80000000u ? fmaf(dot2, iwp, part) : part;
-                    if constexpr (LGW_T > 0) part = group_sum<LGW_T>(part);
-                    else part = group_sum_rt(part, lgw);
-                    // dx into LDS by sorted row (every lane of the group holds
-                    // the same sum; rows past the piece's end: the discard slot)
-                    s_dx[i < n ? rs + i : kP] = part;
+                    parts[i] = dsc[i].x == 0x80000000u ? fmaf(dot2, iwp, part) : part;
+                }
+                // dx into LDS by sorted row (rows past the piece's end: the
+                // discard slot)
+                if constexpr (LGW_T >= 4 && LGW_T <= 16) {
+                    // reduce-scatter: each lane ends with one row's sum
+                    static_assert(kL == 4, "four rows per piece");
+                    constexpr int kLog = LGW_T == 4 ? 2 : (LGW_T == 8 ? 3 : 4);
+                    const int r = (((lc >> (kLog - 1)) & 1) << 1) | ((lc >> (kLog - 2)) & 1);
+                    s_dx[r < n ? rs + r : kP] = group_reduce_scatter4<LGW_T>(parts, lc);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < kL; ++i) {
+                        float v = parts[i];
+                        if constexpr (LGW_T > 0) v = group_sum<LGW_T>(v);
+                        else v = group_sum_rt(v, lgw);
+                        s_dx[i < n ? rs + i : kP] = v;
+                    }
                 }
             };
 
@@ -1118,9 +1131,11 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                     while ((1ll << nbits) <= B) ++nbits;      // keys 0..B
                     geo.nbits = nbits;
                     // chunks of sub-tiles: about PLE_BWD_WG_PER_CU reduce
-                    // workgroups per CU, within the partials budget
+                    // workgroups per CU, within the partials budget.  Two per
+                    // CU measured best at c1-c3 (4 per CU: +15 to +40 us, the
+                    // partials and each workgroup's table staging double)
                     const int64_t per_chunk = F * B * 2 * D * 4;
-                    int64_t c = (static_cast<int64_t>(env_int("PLE_BWD_WG_PER_CU", 4)) * cus + geo.G - 1) / geo.G;
+                    int64_t c = (static_cast<int64_t>(env_int("PLE_BWD_WG_PER_CU", 2)) * cus + geo.G - 1) / geo.G;
                     const int64_t budget_c = static_cast<int64_t>(kPartialBudget) / per_chunk;
                     if (c > budget_c) c = budget_c;
                     if (c > geo.T) c = geo.T;

@@ -239,6 +239,33 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Reduce-scatter of four values per lane over aligned groups of W lanes
+// (W in {4, 8, 16}): returns the group sum of p[r] with r = the lane's row,
+// r = 2 * bit(log2 W - 1) + bit(log2 W - 2) of its index in the group.  Each
+// step exchanges half of what a lane still holds with a partner that differs
+// in one bit -- the partners are XOR masks (mirrors are XOR 15 / XOR 7), so
+// the four steps cover the group exactly once.
+template <int W>
+__device__ __forceinline__ float group_reduce_scatter4(const float (&p)[4], int lc) {
+    static_assert(W == 4 || W == 8 || W == 16, "group width");
+    constexpr int LOG = W == 4 ? 2 : (W == 8 ? 3 : 4);
+    // DPP controls by the bit a partner differs in
+    constexpr int kCtrl[4] = {0xB1, 0x4E, 0x141, 0x140};   // xor 1, xor 2, xor 7 (half-row mirror), xor 15 (row mirror)
+    const bool hi_a = (lc >> (LOG - 1)) & 1;
+    float k0 = hi_a ? p[2] : p[0];
+    float k1 = hi_a ? p[3] : p[1];
+    const float s0 = hi_a ? p[0] : p[2];
+    const float s1 = hi_a ? p[1] : p[3];
+    k0 += dpp_f32<kCtrl[LOG - 1]>(s0);
+    k1 += dpp_f32<kCtrl[LOG - 1]>(s1);
+    const bool hi_b = (lc >> (LOG - 2)) & 1;
+    float k = hi_b ? k1 : k0;
+    k += dpp_f32<kCtrl[LOG - 2]>(hi_b ? k0 : k1);
+    if constexpr (LOG >= 4) k += dpp_f32<kCtrl[1]>(k);
+    if constexpr (LOG >= 3) k += dpp_f32<kCtrl[0]>(k);
+    return k;
+}
+
 // Same, for a group width known only at run time (power of two <= 64).
 __device__ __forceinline__ float group_sum_rt(float v, int w) {
     for (int off = w >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, w);
