@@ -499,6 +499,12 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
             constexpr uint32_t esz = GD == PLE_DTYPE_F32 ? 4 : 2;
             const uint32_t rowFb = static_cast<uint32_t>(F) * D * esz;
             const uint32_t Db = static_cast<uint32_t>(D) * esz;
+            // Gradient rows spanning 128 bytes or more are streamed
+            // (non-temporal loads); narrower rows share lines with a
+            // neighbouring feature's rows, which another run or workgroup
+            // reads later.  (Fixed per instantiation: a branch between the
+            // two forms around the loads costs more than it saves.)
+            constexpr int kGCpol = LGW_T * VEC * static_cast<int>(esz) >= 128 ? kCpolNT : 0;
             const uint32_t span = static_cast<uint32_t>(ns) * rowFb;
             const __amdgpu_buffer_rsrc_t grs = make_rsrc(
                 static_cast<const char *>(a.g) + (sub * F + f0) * static_cast<int64_t>(D) * esz, span);
@@ -535,7 +541,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
                 for (int i = 0; i < kL; ++i) dv[i] = s_sdesc[i < n ? rs + i : kP];
                 // (the 24-bit products ignore the feature bits of .y)
 #pragma unroll
-                for (int i = 0; i < kL; ++i) load_grad_buf<GD, VEC>(grs, __umul24(dv[i].y, rowFb) + flb, gv[i]);
+                for (int i = 0; i < kL; ++i) load_grad_buf<GD, VEC, kGCpol>(grs, __umul24(dv[i].y, rowFb) + flb, gv[i]);
                 if constexpr (kRelu) {
 #pragma unroll
                     for (int i = 0; i < kL; ++i)

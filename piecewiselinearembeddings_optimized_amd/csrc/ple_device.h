@@ -124,36 +124,43 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
                                              static_cast<int>(__builtin_amdgcn_readfirstlane(bytes)), 0x00020000);
 }
 
+// Cache-policy operand of the buffer / global memory builtins: the
+// non-temporal (streaming) hint.  Data read or written once -- the forward's
+// output, gradient rows that fill whole 128-byte lines -- moves through the
+// caches without displacing lines that are reused.
+constexpr int kCpolNT = 2;
+
 // VEC consecutive gradient elements at byte offset `off` of a buffer
-// resource, as floats (VEC in {1, 2, 4, 8}; `off` aligned for the access).
-template <int G, int VEC>
+// resource, as floats (VEC in {1, 2, 4, 8}; `off` aligned for the access);
+// CPOL: cache-policy bits of the loads.
+template <int G, int VEC, int CPOL = 0>
 __device__ __forceinline__ void load_grad_buf(__amdgpu_buffer_rsrc_t rs, uint32_t off, float *out) {
     if constexpr (G == PLE_DTYPE_F32) {
         if constexpr (VEC >= 4) {
 #pragma unroll
             for (int q = 0; q < VEC / 4; ++q) {
-                const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * q, 0, 0);
+                const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * q, 0, CPOL);
                 out[4 * q] = __uint_as_float(v[0]); out[4 * q + 1] = __uint_as_float(v[1]);
                 out[4 * q + 2] = __uint_as_float(v[2]); out[4 * q + 3] = __uint_as_float(v[3]);
             }
         } else if constexpr (VEC == 2) {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, CPOL);
             out[0] = __uint_as_float(v[0]); out[1] = __uint_as_float(v[1]);
         } else {
-            out[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+            out[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, CPOL));
         }
     } else {
         uint32_t w[VEC / 2 > 0 ? VEC / 2 : 1];
         if constexpr (VEC == 8) {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, CPOL);
             w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
         } else if constexpr (VEC == 4) {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, CPOL);
             w[0] = v[0]; w[1] = v[1];
         } else if constexpr (VEC == 2) {
-            w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+            w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, CPOL);
         } else {
-            w[0] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+            w[0] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, CPOL);
         }
 #pragma unroll
         for (int t = 0; t < VEC; ++t) {
@@ -191,25 +198,31 @@ __device__ __forceinline__ void lds_store_vec(float *p, const float *v) {
     }
 }
 
-// Stores VEC consecutive outputs as OUT (VEC in {1, 4}).
+// Stores VEC consecutive outputs as OUT (VEC in {1, 4}), with the
+// non-temporal hint: the output is written once and not read back here.
 template <int OUT, int VEC>
 __device__ __forceinline__ void store_out(void *base, int64_t i, const float *v) {
     if constexpr (OUT == PLE_DTYPE_F32) {
         float *p = static_cast<float *>(base) + i;
-        if constexpr (VEC == 4) *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
-        else p[0] = v[0];
+        if constexpr (VEC == 4) {
+            typedef float f32x4 __attribute__((ext_vector_type(4)));
+            const f32x4 t = {v[0], v[1], v[2], v[3]};
+            __builtin_nontemporal_store(t, reinterpret_cast<f32x4 *>(p));
+        } else {
+            __builtin_nontemporal_store(v[0], p);
+        }
     } else {
         uint16_t h[VEC];
 #pragma unroll
         for (int t = 0; t < VEC; ++t) h[t] = (OUT == PLE_DTYPE_BF16) ? bf16_bits(v[t]) : f16_bits(v[t]);
         uint16_t *p = static_cast<uint16_t *>(base) + i;
         if constexpr (VEC == 4) {
-            uint2 w;
-            w.x = static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16);
-            w.y = static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16);
-            *reinterpret_cast<uint2 *>(p) = w;
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            const u32x2 w = {static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16),
+                             static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16)};
+            __builtin_nontemporal_store(w, reinterpret_cast<u32x2 *>(p));
         } else {
-            p[0] = h[0];
+            __builtin_nontemporal_store(h[0], p);
         }
     }
 }

@@ -91,12 +91,7 @@ __global__ __launch_bounds__(kBlock) void ple_encode_kernel(EncArgs a) {
             float v[W];
 #pragma unroll
             for (int j = 0; j < W; ++j) v[j] = enc_value(kq[j], s_bin[s * F + fq[j]], s_frac[s * F + fq[j]]);
-            float *dst = a.out + (n0 + s) * T + p0;
-            if constexpr (V4) {
-                *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-            } else {
-                dst[0] = v[0];
-            }
+            store_out<PLE_DTYPE_F32, W>(a.out, (n0 + s) * T + p0, v);
         }
     }
 }
