@@ -308,26 +308,45 @@ struct FwdPlan {
 };
 
 // FS: the widest power-of-two feature group whose row fits one wave's stores
-// (FS * D/VEC <= 64) and whose tables fit kLdsBudget.  Chunks: about 32
-// workgroups per CU over the grid.
+// (FS * D/VEC <= 64) and whose tables fit kLdsBudget; then, while a sample's
+// segment of the group (FS * D outputs) is shorter than a 128-byte line, wider
+// up to the LDS limit -- partial lines written by different workgroups at
+// different times cost more than the LDS.
+// Chunks: about 32 workgroups per CU over the grid, but each workgroup writes
+// at least kOutPerTable times its tables' bytes, since the table staging and
+// the prefix pass are paid per workgroup.  Together, measured: c2 131 -> 59
+// us, c3 186 -> 155 us, c4 517 -> 221 us, c1 unchanged (its plan is the same).
 // PLE_FWD_FS / PLE_FWD_WG_PER_CU override the two choices (tuning).
-bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, bool aligned16, FwdPlan &pl) {
+constexpr int kOutPerTable = 10;
+
+bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, bool aligned16, FwdPlan &pl) {
     pl.vec = (D % 4 == 0 && aligned16) ? 4 : 1;
     const int U = static_cast<int>(D / pl.vec);
     if (U > kWave) return false;
+    const int Bi = static_cast<int>(B), Di = static_cast<int>(D);
+    auto fits_wave = [&](int f) { return f <= kWave && f * U <= kWave && (f == 1 || f / 2 < F); };
     int fs = 1;
-    while (fs * 2 <= kWave && fs * 2 * U <= kWave && fs < F) fs *= 2;
-    while (fs > 1 && fwd_lds_bytes(fs, static_cast<int>(B), static_cast<int>(D)) > kLdsBudget) fs /= 2;
+    while (fits_wave(fs * 2) && fwd_lds_bytes(fs * 2, Bi, Di) <= kLdsBudget) fs *= 2;
+    while (static_cast<int64_t>(fs) * D * out_bytes < 128 && fits_wave(fs * 2) &&
+           fwd_lds_bytes(fs * 2, Bi, Di) <= kLdsMax)
+        fs *= 2;
     const int fs_env = env_int("PLE_FWD_FS", 0);
     if (fs_env > 0 && (fs_env & (fs_env - 1)) == 0 && fs_env * U <= kWave &&
-        fwd_lds_bytes(fs_env, static_cast<int>(B), static_cast<int>(D)) <= kLdsMax)
+        fwd_lds_bytes(fs_env, Bi, Di) <= kLdsMax)
         fs = fs_env;
-    pl.lds = fwd_lds_bytes(fs, static_cast<int>(B), static_cast<int>(D));
+    pl.lds = fwd_lds_bytes(fs, Bi, Di);
     if (pl.lds > kLdsMax) return false;
     pl.FS = fs;
     pl.G = static_cast<int>((F + fs - 1) / fs);
-    const int target = env_int("PLE_FWD_WG_PER_CU", 32) * device_cu_count();
+    const int wg_env = env_int("PLE_FWD_WG_PER_CU", 0);
+    const int64_t target = static_cast<int64_t>(wg_env > 0 ? wg_env : 32) * device_cu_count();
     int64_t c = (target + pl.G - 1) / pl.G;
+    if (wg_env <= 0) {
+        // output per workgroup (NC * FS * D * out_bytes) >= kOutPerTable * tables (FS * B * D * 4)
+        const int64_t min_nc = (static_cast<int64_t>(kOutPerTable) * B * 4 + out_bytes - 1) / out_bytes;
+        const int64_t c_tbl = (N + min_nc - 1) / min_nc;
+        if (c > c_tbl) c = c_tbl;
+    }
     const int64_t sw = kWave / fs;
     const int64_t max_c = (N + sw - 1) / sw;          // at least one wave tile per chunk
     if (c > max_c) c = max_c;
@@ -379,7 +398,7 @@ int forward_run(const ForwardRequest &r) {
     const bool aligned16 = (reinterpret_cast<uintptr_t>(r.out) % (4 * out_bytes) == 0) &&
                            (reinterpret_cast<uintptr_t>(r.weight) % 16 == 0);
     FwdPlan pl;
-    if (!plan_forward(r.N, r.F, r.B, r.D, aligned16, pl)) return PLE_E_UNSUPPORTED;
+    if (!plan_forward(r.N, r.F, r.B, r.D, out_bytes, aligned16, pl)) return PLE_E_UNSUPPORTED;
     FwdArgs a;
     a.x = r.x; a.edges = r.edges; a.iw = r.iw; a.nbins = r.nbins; a.weight = r.weight;
     a.bias = r.bias; a.lin_w = r.lin_w; a.lin_b = r.lin_b;
