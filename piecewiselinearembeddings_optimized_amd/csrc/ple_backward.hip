@@ -40,8 +40,8 @@
 //   The chunk's histogram is written once.
 //
 // ple_bwd_dx_transpose_kernel turns the feature-major dx into [N, F];
-// ple_bwd_finalize_kernel sums the chunks in chunk order and takes the
-// suffix over bins.
+// ple_bwd_chunksum_kernel adds the chunk partials in chunk order;
+// ple_bwd_finalize_kernel takes the suffix over bins.
 //
 // No floating-point atomics anywhere, a fixed order for every sum, so results
 // repeat bitwise.
@@ -88,6 +88,7 @@ struct BwdArgs {
     int64_t NC;      // fallback: samples per chunk
     int db_from_buckets;   // finalize: db = sum of the bin buckets (no raw-gradient partials)
     int fin_direct;        // finalize: chunk sums read straight from the partials (no LDS table)
+    int fin_summed;        // finalize: the chunk partials are summed into chunk 0 already
     // sorted path
     int FS, G, NT, T, SPC, PM, LGW, nbits;   // T sub-tiles, SPC sub-tiles per chunk, PM piece capacity
     int so_nb, so_edge, so_iw, so_info, so_rank, so_cnt, so_seg, so_tmp, so_desc, so_piece;   // sort LDS
@@ -875,75 +876,125 @@ __global__ __launch_bounds__(kWave) void ple_bwd_simple_hist_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// chunk sums: the partials of every chunk added, in chunk order, into chunk 0
+// ---------------------------------------------------------------------------
+
+// Partials [Cd][per-chunk elements]; one thread per element of chunk 0, its
+// Cd loads issued eight at a time.  Each element is read and rewritten by one
+// thread only, so the sum lands in place.
+__global__ __launch_bounds__(kBlock) void ple_bwd_chunksum_kernel(float *part, int64_t per_chunk, int Cd) {
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; e < per_chunk;
+         e += static_cast<int64_t>(gridDim.x) * kBlock) {
+        float *base = part + e;
+        float s = 0.0f;
+        int cc = 0;
+        for (; cc + 8 <= Cd; cc += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = base[(cc + u) * per_chunk];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += v[u];
+        }
+        for (; cc < Cd; ++cc) s += base[cc * per_chunk];
+        base[0] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // finalize: one workgroup per (feature, group of kFinCols columns)
 // ---------------------------------------------------------------------------
 
 constexpr int kFinCols = 8;
+constexpr int kFinLoadsInline = 128;   // chunk-sum loads per finalize thread, at most
 
 // Sums the chunk partials of every (bin, column) of the group in chunk order
-// into LDS (every thread's loads issued together), then one lane per column
-// takes the suffix over logical bins: dW[phys(k)] = weighted[k] +
-// sum_{m>k} bucket[m]; slots no bin maps to get 0.  The bias gradient is the
-// sum of the buckets (fp32 gradients) or of its own chunk partials.
+// into LDS (or reads their sums from chunk 0, where ple_bwd_chunksum_kernel
+// left them: many bins or chunks), then kFinLanes lanes per column take the
+// suffix over logical
+// bins, dW[phys(k)] = weighted[k] + sum_{m>k} bucket[m]: each lane sums the
+// buckets of its run of bins, a suffix scan over the lanes gives every run the
+// sum above it, and each lane walks its run from the top.  Slots no bin maps
+// to get 0.  The bias gradient is the sum of all buckets (fp32 gradients) or
+// its own summed partials.  A fixed order throughout: results repeat bitwise.
+constexpr int kFinLanes = kBlock / kFinCols;   // lanes per column (half a wave)
+
 __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
     extern __shared__ float tot[];       // [n][2][kFinCols]
     const int f = blockIdx.x;
     const int j0 = blockIdx.y * kFinCols;
-    const int B = a.B, D = a.D, F = a.F;
+    const int B = a.B, D = a.D;
     const int D2 = 2 * D;
     const int nc = min(kFinCols, D - j0);
     const int n = clamp_nbins(a.nbins[f], B);
     const int tid = threadIdx.x;
-    const int64_t cstride = static_cast<int64_t>(F) * B * D2;
     const float *src = a.part + static_cast<int64_t>(f) * B * D2;
     const bool need_tot = !a.fin_direct && (a.dw || (a.db && a.db_from_buckets));
-    // bin k's chunk sum of half h (0: bucket, 1: weighted) for this thread's column
+    const int col = tid / kFinLanes;
+    const int l = tid % kFinLanes;
+    // bin k's chunk sum of half h (0: bucket, 1: weighted) for this lane's column
+    // (fin_direct implies summed chunks)
     auto total = [&](int k, int h) {
-        if (!a.fin_direct) return tot[(k * 2 + h) * kFinCols + tid];
-        const float *p = src + k * D2 + h * D + j0 + tid;
-        float s = 0.0f;
-        for (int cc = 0; cc < a.Cd; ++cc) s += p[cc * cstride];
-        return s;
+        if (!a.fin_direct) return tot[(k * 2 + h) * kFinCols + col];
+        return src[k * D2 + h * D + j0 + col];
     };
+    const int nsum = a.fin_summed ? 1 : a.Cd;
+    const int64_t cstride = static_cast<int64_t>(a.F) * B * D2;
     if (need_tot) {
         // element e -> (bin k, half h: bucket / weighted, column j0 + c)
         for (int e = tid; e < n * 2 * kFinCols; e += kBlock) {
             const int k = e / (2 * kFinCols);
             const int h = (e / kFinCols) & 1;
             const int cidx = e % kFinCols;
-            float s = 0.0f;
+            float sum = 0.0f;
             if (cidx < nc) {
                 const float *p = src + k * D2 + h * D + j0 + cidx;
 #pragma unroll 8
-                for (int cc = 0; cc < a.Cd; ++cc) s += p[cc * cstride];
+                for (int cc = 0; cc < nsum; ++cc) sum += p[cc * cstride];
             }
-            tot[e] = s;
+            tot[e] = sum;
         }
         __syncthreads();
     }
-    if (tid < nc) {
-        const int j = j0 + tid;
+    if (col >= nc) return;   // (whole half-waves: the scan below stays within live lanes)
+    const int j = j0 + col;
+    const int64_t wrow = static_cast<int64_t>(f) * B;
+    const bool sum_buckets = a.dw || (a.db && a.db_from_buckets);
+    if (sum_buckets) {
+        const int m = (n + kFinLanes - 1) / kFinLanes;   // bins per lane
+        const int lo = min(n, l * m);
+        const int hi = min(n, lo + m);
+        float run = 0.0f;
+        for (int k = hi - 1; k >= lo; --k) run += total(k, 0);
+        // inclusive suffix over the lanes: sum of the runs of lanes l, l+1, ...
+        float incl = run;
+#pragma unroll
+        for (int off = 1; off < kFinLanes; off <<= 1) {
+            const float t = __shfl_down(incl, off, kFinLanes);
+            if (l + off < kFinLanes) incl += t;
+        }
+        const float above = __shfl_down(incl, 1, kFinLanes);
         if (a.dw) {
-            float fut = 0.0f;
-            for (int k = n - 1; k >= 0; --k) {
-                a.dw[(static_cast<int64_t>(f) * B + phys_bin(k, n, B)) * D + j] = total(k, 1) + fut;
+            float fut = l + 1 < kFinLanes ? above : 0.0f;
+            for (int k = hi - 1; k >= lo; --k) {
+                a.dw[(wrow + phys_bin(k, n, B)) * D + j] = total(k, 1) + fut;
                 fut += total(k, 0);
             }
-            for (int k = n - 1; k < B - 1; ++k) a.dw[(static_cast<int64_t>(f) * B + k) * D + j] = 0.0f;
+            for (int k = n - 1 + l; k < B - 1; k += kFinLanes) a.dw[(wrow + k) * D + j] = 0.0f;
         }
-        if (a.db) {
+        if (a.db && a.db_from_buckets && l == 0) a.db[static_cast<int64_t>(f) * D + j] = incl;
+    }
+    if (l == 0) {
+        const int64_t fj = static_cast<int64_t>(f) * D + j;
+        const int64_t dstride = static_cast<int64_t>(a.F) * D;
+        if (a.db && !a.db_from_buckets) {
             float sb = 0.0f;
-            if (a.db_from_buckets) {
-                for (int k = n - 1; k >= 0; --k) sb += total(k, 0);
-            } else {
-                for (int cc = 0; cc < a.Cd; ++cc) sb += a.part_db[(static_cast<int64_t>(cc) * F + f) * D + j];
-            }
-            a.db[static_cast<int64_t>(f) * D + j] = sb;
+            for (int cc = 0; cc < a.Cd; ++cc) sb += a.part_db[cc * dstride + fj];
+            a.db[fj] = sb;
         }
         if (a.dlw) {
             float sl = 0.0f;
-            for (int cc = 0; cc < a.Cd; ++cc) sl += a.part_lw[(static_cast<int64_t>(cc) * F + f) * D + j];
-            a.dlw[static_cast<int64_t>(f) * D + j] = sl;
+            for (int cc = 0; cc < a.Cd; ++cc) sl += a.part_lw[cc * dstride + fj];
+            a.dlw[fj] = sl;
         }
     }
 }
@@ -1274,6 +1325,20 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
         size_t lds = static_cast<size_t>(a.B) * 2 * kFinCols * sizeof(float);
         a.fin_direct = lds > kLdsMax;          // very many bins: no LDS table
         if (a.fin_direct) lds = 0;
+        // The finalize sums the chunks itself unless a thread would issue more
+        // than kFinLoadsInline loads; then a wide kernel sums them first.
+        const int64_t loads = static_cast<int64_t>(a.B) * 2 * kFinCols * a.Cd / kBlock;
+        a.fin_summed = a.Cd > 1 && (a.fin_direct || loads > kFinLoadsInline);
+        if (a.fin_summed) {
+            const int64_t per_chunk = static_cast<int64_t>(a.F) * a.B * 2 * a.D;
+            int64_t blocks = (per_chunk + kBlock - 1) / kBlock;
+            const int64_t cap = static_cast<int64_t>(device_cu_count()) * 32;
+            if (blocks > cap) blocks = cap;
+            hipLaunchKernelGGL(ple_bwd_chunksum_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, a.part,
+                               per_chunk, a.Cd);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
         const dim3 fg(static_cast<unsigned>(a.F), static_cast<unsigned>((a.D + kFinCols - 1) / kFinCols));
         hipLaunchKernelGGL(ple_bwd_finalize_kernel, fg, dim3(kBlock), lds, s, a);
         e = hipGetLastError();
