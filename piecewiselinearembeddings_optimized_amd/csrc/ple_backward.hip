@@ -34,8 +34,9 @@
 //   weighted / bias sums run in registers until the key changes (checked
 //   once per piece).  A run's first key goes to a per-run record, every
 //   later key straight into the LDS histogram (no other run can own it); the
-//   records are added run by run in order.  The sub-tile's dx leaves
-//   feature-major through an inverse permutation (whole-line stores).  The
+//   records are added run by run in order.  Each row's dx is staged in LDS
+//   at its pair's position (the descriptor names it) and leaves
+//   feature-major in whole lines.  The
 //   next sub-tile's descriptors travel while the current one is reduced.
 //   The chunk's histogram is written once.
 //
@@ -92,7 +93,7 @@ struct BwdArgs {
     // sorted path
     int FS, G, NT, T, SPC, PM, LGW, nbits;   // T sub-tiles, SPC sub-tiles per chunk, PM piece capacity
     int so_nb, so_edge, so_iw, so_info, so_rank, so_cnt, so_seg, so_tmp, so_desc, so_piece;   // sort LDS
-    int ro_qw, ro_hist, ro_db, ro_iw, ro_nb, ro_desc, ro_piece, ro_npc, ro_rec, ro_rkey, ro_rfl, ro_dx, ro_inv,
+    int ro_qw, ro_hist, ro_db, ro_iw, ro_nb, ro_desc, ro_piece, ro_npc, ro_rec, ro_rkey, ro_rfl, ro_dx,
         ro_lw, ro_dlw;   // reduce LDS
 };
 
@@ -320,8 +321,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
     float *s_rec = reinterpret_cast<float *>(lds + a.ro_rec);           // [LG][RS]
     int *s_rkey = reinterpret_cast<int *>(lds + a.ro_rkey);             // [LG]
     int *s_rfl = reinterpret_cast<int *>(lds + a.ro_rfl);               // [LG]
-    float *s_dx = reinterpret_cast<float *>(lds + a.ro_dx);             // [P+1] dx by sorted row (+ a discard slot)
-    uint16_t *s_inv = reinterpret_cast<uint16_t *>(lds + a.ro_inv);     // [P] sorted row of each pair
+    float *s_dx = reinterpret_cast<float *>(lds + a.ro_dx);             // [P+1] dx by pair, fl * NT + s (+ a discard slot)
     float *s_lw = reinterpret_cast<float *>(lds + a.ro_lw);             // [FS][D] linear0 weight
     float *s_dlw = reinterpret_cast<float *>(lds + a.ro_dlw);           // [FS][D] sum of g x
 
@@ -400,6 +400,11 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
     // record stride {bucket | weighted (| raw g) (| g x)}
     const int RS = (kRawDb ? 3 * D : 2 * D) + (kLin ? D : 0);
     const int nt_shift = __ffs(NT) - 1;           // NT is a power of two
+    // dx slot of a row: its pair's position (feature-major, fl * NT + s), so
+    // that the sub-tile's dx leaves in pair order
+    auto dx_slot = [&](uint32_t y) __attribute__((always_inline)) {
+        return static_cast<int>(((y >> 24) << nt_shift) + (y & 0xffffff));
+    };
 
     for (int t = t_begin; t < t_end; ++t) {
         // the previous sub-tile's pieces are reduced and its records merged
@@ -414,13 +419,6 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
         __syncthreads();
         // (past the chunk's last sub-tile: the same sub-tile again, unused)
         PLE_PREFETCH(t + 1 < t_end ? t + 1 : t);
-        // sorted row of each pair, for the dx stores (read after F's barrier)
-#pragma unroll
-        for (int u = 0; u < kPairsPerThread; ++u) {
-            const int r = tid + u * kBlock;
-            const uint32_t y = s_sdesc[r].y;
-            s_inv[((y >> 24) << nt_shift) + (y & 0xffffff)] = static_cast<uint16_t>(r);
-        }
         const int64_t sub = static_cast<int64_t>(t) * NT;
         const int ns = static_cast<int>(min(static_cast<int64_t>(NT), a.N - sub));
 
@@ -592,7 +590,6 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
                     iwk = s_iw[rowbase + k];
                     iwp = s_iw[rowbase + kp];
                 }
-                const int rs = static_cast<int>((pe >> 16) & 0xfff);
                 float parts[kL];
 #pragma unroll
                 for (int i = 0; i < kL; ++i) {
@@ -630,14 +627,18 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
                     static_assert(kL == 4, "four rows per piece");
                     constexpr int kLog = LGW_T == 4 ? 2 : (LGW_T == 8 ? 3 : 4);
                     const int r = (((lc >> (kLog - 1)) & 1) << 1) | ((lc >> (kLog - 2)) & 1);
-                    s_dx[r < n ? rs + r : kP] = group_reduce_scatter4<LGW_T>(parts, lc);
+                    // (selects on named values: indexing the descriptor array
+                    // with r would put it in scratch memory)
+                    const uint32_t y0 = dsc[0].y, y1 = dsc[1].y, y2 = dsc[2].y, y3 = dsc[3].y;
+                    const uint32_t yr = (r & 2) ? ((r & 1) ? y3 : y2) : ((r & 1) ? y1 : y0);
+                    s_dx[r < n ? dx_slot(yr) : kP] = group_reduce_scatter4<LGW_T>(parts, lc);
                 } else {
 #pragma unroll
                     for (int i = 0; i < kL; ++i) {
                         float v = parts[i];
                         if constexpr (LGW_T > 0) v = group_sum<LGW_T>(v);
                         else v = group_sum_rt(v, lgw);
-                        s_dx[i < n ? rs + i : kP] = v;
+                        s_dx[i < n ? dx_slot(dsc[i].y) : kP] = v;
                     }
                 }
             };
@@ -674,7 +675,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
                 const int p = tid + u * kBlock;
                 const int fl = p >> nt_shift;
                 const int sidx = p & (NT - 1);
-                if (fl < nfh && sidx < ns) a.dxt[static_cast<int64_t>(f0 + fl) * a.N + sub + sidx] = s_dx[s_inv[p]];
+                if (fl < nfh && sidx < ns) a.dxt[static_cast<int64_t>(f0 + fl) * a.N + sub + sidx] = s_dx[p];
             }
         }
 
@@ -1118,7 +1119,6 @@ size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_
     take(g.ro_rkey, 4ull * LG);
     take(g.ro_rfl, 4ull * LG);
     take(g.ro_dx, 4ull * (kP + 1));
-    take(g.ro_inv, 2ull * kP);
     take(g.ro_lw, lin ? 4ull * FS * D : 0ull);
     take(g.ro_dlw, lin ? 4ull * FS * D : 0ull);
     return take.off;
