@@ -90,6 +90,7 @@ struct BwdArgs {
     int db_from_buckets;   // finalize: db = sum of the bin buckets (no raw-gradient partials)
     int fin_direct;        // finalize: chunk sums read straight from the partials (no LDS table)
     int fin_summed;        // finalize: the chunk partials are summed into chunk 0 already
+    int dbuf;              // reduce: two LDS buffers for the sub-tile descriptors
     // sorted path
     int FS, G, NT, T, SPC, PM, LGW, nbits;   // T sub-tiles, SPC sub-tiles per chunk, PM piece capacity
     int so_nb, so_edge, so_iw, so_info, so_rank, so_cnt, so_seg, so_tmp, so_desc, so_piece;   // sort LDS
@@ -315,9 +316,9 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
     float *s_db = reinterpret_cast<float *>(lds + a.ro_db);             // [FS][D]
     float *s_iw = reinterpret_cast<float *>(lds + a.ro_iw);             // [FS][B]
     int *s_nb = reinterpret_cast<int *>(lds + a.ro_nb);                 // [FS]
-    uint2 *s_sdesc = reinterpret_cast<uint2 *>(lds + a.ro_desc);        // [P+1]: sorted rows, then a dummy row
-    uint32_t *s_piece = reinterpret_cast<uint32_t *>(lds + a.ro_piece); // [PM]
-    int *s_npc = reinterpret_cast<int *>(lds + a.ro_npc);               // [1]
+    uint2 *s_sdesc = reinterpret_cast<uint2 *>(lds + a.ro_desc);        // [1|2][P+1]: sorted rows, then a dummy row
+    uint32_t *s_piece = reinterpret_cast<uint32_t *>(lds + a.ro_piece); // [1|2][PM]
+    int *s_npc = reinterpret_cast<int *>(lds + a.ro_npc);               // [1|2]
     float *s_rec = reinterpret_cast<float *>(lds + a.ro_rec);           // [LG][RS]
     int *s_rkey = reinterpret_cast<int *>(lds + a.ro_rkey);             // [LG]
     int *s_rfl = reinterpret_cast<int *>(lds + a.ro_rfl);               // [LG]
@@ -360,9 +361,12 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
     PLE_PREFETCH(t_begin);
 
     // ---- stage tables, clear accumulators ---------------------------------
-    // Rows past a piece's end read the dummy row kP: q(frac) = +0 and sample
+    // Rows past a piece's end read the dummy row kP of their buffer: q(frac) = +0 and sample
     // NT, whose gradient offset lies past every sub-tile's span (zeros).
-    if (tid == 0) s_sdesc[kP] = make_uint2(0u, static_cast<uint32_t>(NT));
+    if (tid == 0) {
+        s_sdesc[kP] = make_uint2(0u, static_cast<uint32_t>(NT));
+        if (a.dbuf) s_sdesc[2 * kP + 1] = make_uint2(0u, static_cast<uint32_t>(NT));
+    }
     for (int i = tid; i < FS; i += kBlock) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
     for (int i = tid; i < FS * B; i += kBlock) {
         const int fl = i / B;
@@ -406,267 +410,298 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
         return static_cast<int>(((y >> 24) << nt_shift) + (y & 0xffffff));
     };
 
-    for (int t = t_begin; t < t_end; ++t) {
-        // the previous sub-tile's pieces are reduced and its records merged
-        reinterpret_cast<uint4 *>(s_sdesc)[tid] = pd0;
-        reinterpret_cast<uint4 *>(s_sdesc)[tid + kBlock] = pd1;
-        if (tid < PM) s_piece[tid] = pp0;
-        if (tid + kBlock < PM) s_piece[tid + kBlock] = pp1;
-        if (tid + 2 * kBlock < PM) s_piece[tid + 2 * kBlock] = pp2;
-        if (tid + 3 * kBlock < PM) s_piece[tid + 3 * kBlock] = pp3;
-        if (tid + 4 * kBlock < PM) s_piece[tid + 4 * kBlock] = pp4;
-        if (tid == 0) s_npc[0] = pnpc;
-        __syncthreads();
-        // (past the chunk's last sub-tile: the same sub-tile again, unused)
+    // F-phase state of a run: running sums of its current key (feature,
+    // bin) -- packed as fl << 12 | k -- and, with rounding quantisation, of
+    // its feature.  Rows past a piece's end and idle lanes (lc >= D / VEC)
+    // load from past the end of the gradient buffer, which reads zeros: they
+    // add nothing and need no masking.
+    int cur = -1, db_fl = -1;
+    bool first_key = true, first_fl = true;
+    float ab[VEC], aw[VEC], ad[VEC], ax[VEC];
+    float *rec = s_rec + lg * RS + lc * VEC;
+
+    // first key of the run -> record; later keys -> straight into the
+    // histogram (this run is their only writer).  One read-modify-write
+    // through a selected pointer keeps the code inlined per piece small.
+    auto flush_key = [&]() __attribute__((always_inline)) {
+        if (cur < 0) return;
+        float *h = s_hist + __umul24(__umul24(cur >> 12, B) + (cur & 0xfff), D2) + lc * VEC;
+        float *dst = first_key ? rec : h;
+        if (c_ok) {
+            float ob[VEC], ow[VEC];
+            lds_load_vec<VEC>(dst, ob);
+            lds_load_vec<VEC>(dst + D, ow);
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) {
+                ob[q] = first_key ? ab[q] : ob[q] + ab[q];
+                ow[q] = first_key ? aw[q] : ow[q] + aw[q];
+            }
+            lds_store_vec<VEC>(dst, ob);
+            lds_store_vec<VEC>(dst + D, ow);
+        }
+        if (first_key && lc == 0) s_rkey[lg] = cur;
+        first_key = false;
+    };
+    auto flush_fl = [&]() __attribute__((always_inline)) {
+        if (db_fl < 0) return;
+        float *dst = first_fl ? rec + D2 : s_db + db_fl * D + lc * VEC;
+        if (c_ok) {
+            float o[VEC];
+            lds_load_vec<VEC>(dst, o);
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) o[q] = first_fl ? ad[q] : o[q] + ad[q];
+            lds_store_vec<VEC>(dst, o);
+            if constexpr (kLin) {
+                float *dx2 = first_fl ? rec + D2 + D : s_dlw + db_fl * D + lc * VEC;
+                lds_load_vec<VEC>(dx2, o);
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) o[q] = first_fl ? ax[q] : o[q] + ax[q];
+                lds_store_vec<VEC>(dx2, o);
+            }
+        }
+        if (first_fl && lc == 0) s_rfl[lg] = db_fl;
+        first_fl = false;
+    };
+
+    // The current sub-tile: its descriptor and piece buffers, lane group
+    // lg's run of contiguous pieces [j0, j1) (m pieces per run, the same for
+    // every run), and its gradient rows as one buffer resource: byte offset
+    // s * rowFb + fl * Db + lane offset (24-bit products: the planner keeps
+    // the sub-tile's span below 2^31 bytes).  Offset `span` (first byte past
+    // the sub-tile) stands in for rows past a piece's end and for idle lanes.
+    constexpr uint32_t esz = GD == PLE_DTYPE_F32 ? 4 : 2;
+    const uint32_t rowFb = static_cast<uint32_t>(F) * D * esz;
+    const uint32_t Db = static_cast<uint32_t>(D) * esz;
+    // Gradient rows spanning 128 bytes or more are streamed (non-temporal
+    // loads); narrower rows share lines with a neighbouring feature's rows,
+    // which another run or workgroup reads later.  (Fixed per instantiation:
+    // a branch between the two forms around the loads costs more than it
+    // saves.)
+    constexpr int kGCpol = LGW_T * VEC * static_cast<int>(esz) >= 128 ? kCpolNT : 0;
+    // idle lanes: an offset past every span
+    const uint32_t laneoff = c_ok ? static_cast<uint32_t>(lc) * VEC * esz : 0x80000000u;
+    // epilogue inputs of a row (sample s, local feature fl): its mask word
+    // (the one holding this lane's columns) and x; rows past a piece's end
+    // (sample NT) read zeros
+    const int MW = a.MW;
+    const uint32_t rowMb = static_cast<uint32_t>(F) * MW * 4;
+    const uint32_t m_word_off = static_cast<uint32_t>((lcx * VEC) >> 5) * 4;
+    const int m_shift = (lcx * VEC) & 31;
+    const uint2 *t_desc = s_sdesc;
+    const uint32_t *t_piece = s_piece;
+    int64_t sub = 0;
+    int ns = 0, m = 0, j0 = 0, j1 = 0;
+    __amdgpu_buffer_rsrc_t grs = make_rsrc(a.g, 0u), mrs = grs, xrs = grs;
+    // sub-tile t, staged in LDS buffer b, becomes the current one
+    auto set_tile = [&](int t, int b) __attribute__((always_inline)) {
+        t_desc = s_sdesc + b * (kP + 1);
+        t_piece = s_piece + b * PM;
+        // (the same for every lane: kept in a scalar register, so the piece
+        // loop's branches are scalar)
+        const int NPc = __builtin_amdgcn_readfirstlane(s_npc[b]);
+        m = (NPc + LG - 1) / LG;
+        j0 = lg * m;
+        j1 = min(j0 + m, NPc);
+        sub = static_cast<int64_t>(t) * NT;
+        ns = static_cast<int>(min(static_cast<int64_t>(NT), a.N - sub));
+        const int64_t row0 = sub * F + f0;
+        grs = make_rsrc(static_cast<const char *>(a.g) + row0 * static_cast<int64_t>(D) * esz,
+                        static_cast<uint32_t>(ns) * rowFb);
+        if constexpr (kRelu) mrs = make_rsrc(a.mask + row0 * MW, static_cast<uint32_t>(ns) * F * MW * 4);
+        if constexpr (kLin) xrs = make_rsrc(a.x + row0, static_cast<uint32_t>(ns) * F * 4);
+    };
+    // the prefetched sub-tile's descriptors, pieces and piece count from the
+    // prefetch registers into LDS buffer b
+    auto stash = [&](int b) __attribute__((always_inline)) {
+        uint2 *dd = s_sdesc + b * (kP + 1);
+        uint32_t *pp = s_piece + b * PM;
+        reinterpret_cast<uint4 *>(dd)[tid] = pd0;
+        reinterpret_cast<uint4 *>(dd)[tid + kBlock] = pd1;
+        if (tid < PM) pp[tid] = pp0;
+        if (tid + kBlock < PM) pp[tid + kBlock] = pp1;
+        if (tid + 2 * kBlock < PM) pp[tid + 2 * kBlock] = pp2;
+        if (tid + 3 * kBlock < PM) pp[tid + 3 * kBlock] = pp3;
+        if (tid + 4 * kBlock < PM) pp[tid + 4 * kBlock] = pp4;
+        if (tid == 0) s_npc[b] = pnpc;
+    };
+
+    // Piece tt of the current sub-tile's run: its entry, its rows'
+    // descriptors, and loads of their gradient rows.  Past j1 the piece is
+    // empty (all rows read zeros).  Every lane loads, with no branch around the load,
+    // so each piece has one counted wait.
+    auto issue = [&](int tt, float (&gv)[kL][VEC], uint2 (&dv)[kL], uint32_t &pe, uint32_t (&mv)[kL],
+                     float (&xv)[kL]) __attribute__((always_inline)) {
+        const int j = j0 + tt;
+        const bool real = j < j1;
+        pe = t_piece[real ? j : 0];
+        const int rs = static_cast<int>((pe >> 16) & 0xfff);
+        const int n = real ? static_cast<int>(pe >> 28) + 1 : 0;
+        const uint32_t flp = (pe >> 12) & 0xf;
+        const uint32_t flb = __umul24(flp, Db) + laneoff;
+#pragma unroll
+        for (int i = 0; i < kL; ++i) dv[i] = t_desc[i < n ? rs + i : kP];
+        // (the 24-bit products ignore the feature bits of .y)
+#pragma unroll
+        for (int i = 0; i < kL; ++i) load_grad_buf<GD, VEC, kGCpol>(grs, __umul24(dv[i].y, rowFb) + flb, gv[i]);
+        if constexpr (kRelu) {
+#pragma unroll
+            for (int i = 0; i < kL; ++i)
+                mv[i] = __builtin_amdgcn_raw_buffer_load_b32(
+                    mrs, __umul24(dv[i].y, rowMb) + flp * static_cast<uint32_t>(MW) * 4 + m_word_off, 0, 0);
+        }
+        if constexpr (kLin) {
+#pragma unroll
+            for (int i = 0; i < kL; ++i)
+                xv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    xrs, __umul24(dv[i].y, static_cast<uint32_t>(F) * 4) + flp * 4, 0, 0));
+        }
+    };
+
+    // weight rows k and k-1 and their inverse widths for the current
+    // key, reloaded from LDS when the key changes (idle lanes read
+    // column 0; their g is 0); row k-1 serves rows with x on e_k
+    float wk[VEC], wp[VEC], lw[VEC];
+    float iwk = 0.0f, iwp = 0.0f;
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) wk[q] = wp[q] = lw[q] = 0.0f;
+    auto process = [&](int tt, const float (&gv)[kL][VEC], const uint2 (&dsc)[kL], uint32_t pe,
+                       const uint32_t (&mv)[kL], const float (&xv)[kL]) __attribute__((always_inline)) {
+        const bool real = j0 + tt < j1;
+        const int n = real ? static_cast<int>(pe >> 28) + 1 : 0;
+        const int key = real ? static_cast<int>(pe & 0xffff) : cur;
+        const int fl = key >> 12;
+        if (key != cur) {
+            flush_key();
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) ab[q] = aw[q] = 0.0f;
+            if constexpr (kRawDb) {
+                if (fl != db_fl) {
+                    flush_fl();
+#pragma unroll
+                    for (int q = 0; q < VEC; ++q) ad[q] = ax[q] = 0.0f;
+                    db_fl = fl;
+                }
+            }
+            if constexpr (kLin) lds_load_vec<VEC>(s_lw + __umul24(fl, D) + lcx * VEC, lw);
+            cur = key;
+            const int k = key & 0xfff;
+            const int kp = k > 0 ? k - 1 : 0;
+            const int rowbase = __umul24(fl, B);
+            lds_load_vec<VEC>(s_qw + __umul24(rowbase + k, D) + lcx * VEC, wk);
+            lds_load_vec<VEC>(s_qw + __umul24(rowbase + kp, D) + lcx * VEC, wp);
+            iwk = s_iw[rowbase + k];
+            iwp = s_iw[rowbase + kp];
+        }
+        float parts[kL];
+#pragma unroll
+        for (int i = 0; i < kL; ++i) {
+            const float qf = __uint_as_float(dsc[i].x);
+            float gq[VEC], gm[VEC];
+            float dot = 0.0f, dot2 = 0.0f, dotl = 0.0f;
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) {
+                // ReLU: the forward's pass bit of column lc * VEC + q
+                gm[q] = gv[i][q];
+                if constexpr (kRelu)
+                    gm[q] = __uint_as_float(__float_as_uint(gm[q]) &
+                                            static_cast<uint32_t>(__builtin_amdgcn_sbfe(
+                                                static_cast<int>(mv[i]), m_shift + q, 1)));
+                gq[q] = quant<Q>(gm[q]);
+                ab[q] += gq[q];
+                aw[q] = fmaf(qf, gq[q], aw[q]);
+                if constexpr (kRawDb) ad[q] += kLin ? gv[i][q] : gm[q];
+                if constexpr (kLin) {
+                    ax[q] = fmaf(gv[i][q], xv[i], ax[q]);
+                    dotl = fmaf(gv[i][q], lw[q], dotl);
+                }
+                dot = fmaf(gq[q], wk[q], dot);
+                dot2 = fmaf(gq[q], wp[q], dot2);
+            }
+            float part = dot * iwk;
+            if constexpr (kLin) part += dotl;
+            // x on the bin's left edge (k >= 1): the lower bin's term too
+            parts[i] = dsc[i].x == 0x80000000u ? fmaf(dot2, iwp, part) : part;
+        }
+        // dx into LDS by sorted row (rows past the piece's end: the
+        // discard slot)
+        if constexpr (LGW_T >= 4 && LGW_T <= 16) {
+            // reduce-scatter: each lane ends with one row's sum
+            static_assert(kL == 4, "four rows per piece");
+            constexpr int kLog = LGW_T == 4 ? 2 : (LGW_T == 8 ? 3 : 4);
+            const int r = (((lc >> (kLog - 1)) & 1) << 1) | ((lc >> (kLog - 2)) & 1);
+            // (selects on named values: indexing the descriptor array
+            // with r would put it in scratch memory)
+            const uint32_t y0 = dsc[0].y, y1 = dsc[1].y, y2 = dsc[2].y, y3 = dsc[3].y;
+            const uint32_t yr = (r & 2) ? ((r & 1) ? y3 : y2) : ((r & 1) ? y1 : y0);
+            s_dx[r < n ? dx_slot(yr) : kP] = group_reduce_scatter4<LGW_T>(parts, lc);
+        } else {
+#pragma unroll
+            for (int i = 0; i < kL; ++i) {
+                float v = parts[i];
+                if constexpr (LGW_T > 0) v = group_sum<LGW_T>(v);
+                else v = group_sum_rt(v, lgw);
+                s_dx[i < n ? dx_slot(dsc[i].y) : kP] = v;
+            }
+        }
+    };
+
+    // Two register buffers: piece tt+1 is in flight while piece tt is
+    // reduced.  m is the same for every run, so the loop is uniform; a piece
+    // issued past a run's end is empty.  A sub-tile's first piece is issued
+    // as soon as its descriptors are in LDS: with two LDS buffers (dbuf)
+    // before the previous sub-tile's dx stores and record merge, with one
+    // after them.
+    float gA[kL][VEC], gB[kL][VEC];
+    uint2 dA[kL], dB[kL];
+    uint32_t pA = 0, pB = 0;
+    uint32_t mA[kL], mB[kL];     // (epilogue with ReLU)
+    float xA[kL], xB[kL];        // (epilogue with linear0)
+    const bool dbuf = a.dbuf != 0;
+    auto begin_tile = [&](int t, int b) __attribute__((always_inline)) {
+        // (past the chunk's last sub-tile: the last one again, unused)
         PLE_PREFETCH(t + 1 < t_end ? t + 1 : t);
-        const int64_t sub = static_cast<int64_t>(t) * NT;
-        const int ns = static_cast<int>(min(static_cast<int64_t>(NT), a.N - sub));
+        set_tile(t, b);
+        if (m > 0) issue(0, gA, dA, pA, mA, xA);
+    };
+
+    stash(0);
+    __syncthreads();
+    begin_tile(t_begin, 0);
+    for (int t = t_begin; t < t_end; ++t) {
+        const int b = dbuf ? (t - t_begin) & 1 : 0;
 
         // F. pieces: lane group lg takes the contiguous pieces [j0, j1) (its
-        //    "run"), the next piece's gradient rows in flight while the
-        //    current one is reduced
-        {
-            // Running sums of the run's current key (feature, bin) -- packed as
-            // fl << 12 | k -- and, with rounding quantisation, of its feature.
-            // Rows past a piece's end and idle lanes (lc >= D / VEC) load from
-            // past the end of the gradient buffer, which reads zeros: they add
-            // nothing and need no masking.
-            int cur = -1, db_fl = -1;
-            bool first_key = true, first_fl = true;
-            float ab[VEC], aw[VEC], ad[VEC], ax[VEC];
+        //    "run"); piece 0 is in flight already
+        cur = -1;
+        db_fl = -1;
+        first_key = first_fl = true;
 #pragma unroll
-            for (int q = 0; q < VEC; ++q) ab[q] = aw[q] = ad[q] = ax[q] = 0.0f;
-            if (lc == 0) {
-                s_rkey[lg] = -1;
-                s_rfl[lg] = -1;
-            }
-            float *rec = s_rec + lg * RS + lc * VEC;
-
-            // first key of the run -> record; later keys -> straight into the
-            // histogram (this run is their only writer).  One read-modify-write
-            // through a selected pointer keeps the code inlined per piece small.
-            auto flush_key = [&]() __attribute__((always_inline)) {
-                if (cur < 0) return;
-                float *h = s_hist + __umul24(__umul24(cur >> 12, B) + (cur & 0xfff), D2) + lc * VEC;
-                float *dst = first_key ? rec : h;
-                if (c_ok) {
-                    float ob[VEC], ow[VEC];
-                    lds_load_vec<VEC>(dst, ob);
-                    lds_load_vec<VEC>(dst + D, ow);
-#pragma unroll
-                    for (int q = 0; q < VEC; ++q) {
-                        ob[q] = first_key ? ab[q] : ob[q] + ab[q];
-                        ow[q] = first_key ? aw[q] : ow[q] + aw[q];
-                    }
-                    lds_store_vec<VEC>(dst, ob);
-                    lds_store_vec<VEC>(dst + D, ow);
-                }
-                if (first_key && lc == 0) s_rkey[lg] = cur;
-                first_key = false;
-            };
-            auto flush_fl = [&]() __attribute__((always_inline)) {
-                if (db_fl < 0) return;
-                float *dst = first_fl ? rec + D2 : s_db + db_fl * D + lc * VEC;
-                if (c_ok) {
-                    float o[VEC];
-                    lds_load_vec<VEC>(dst, o);
-#pragma unroll
-                    for (int q = 0; q < VEC; ++q) o[q] = first_fl ? ad[q] : o[q] + ad[q];
-                    lds_store_vec<VEC>(dst, o);
-                    if constexpr (kLin) {
-                        float *dx2 = first_fl ? rec + D2 + D : s_dlw + db_fl * D + lc * VEC;
-                        lds_load_vec<VEC>(dx2, o);
-#pragma unroll
-                        for (int q = 0; q < VEC; ++q) o[q] = first_fl ? ax[q] : o[q] + ax[q];
-                        lds_store_vec<VEC>(dx2, o);
-                    }
-                }
-                if (first_fl && lc == 0) s_rfl[lg] = db_fl;
-                first_fl = false;
-            };
-
-            const int NPc = s_npc[0];
-            const int m = (NPc + LG - 1) / LG;           // pieces per run
-            const int j0 = lg * m;
-            const int j1 = min(j0 + m, NPc);
-
-            // The sub-tile's gradient rows as one buffer resource: byte offset
-            // s * rowFb + fl * Db + lane offset (24-bit products: the planner
-            // keeps the sub-tile's span below 2^31 bytes).  Offset `span`
-            // (first byte past the sub-tile) stands in for rows past a piece's
-            // end and for idle lanes.
-            constexpr uint32_t esz = GD == PLE_DTYPE_F32 ? 4 : 2;
-            const uint32_t rowFb = static_cast<uint32_t>(F) * D * esz;
-            const uint32_t Db = static_cast<uint32_t>(D) * esz;
-            // Gradient rows spanning 128 bytes or more are streamed
-            // (non-temporal loads); narrower rows share lines with a
-            // neighbouring feature's rows, which another run or workgroup
-            // reads later.  (Fixed per instantiation: a branch between the
-            // two forms around the loads costs more than it saves.)
-            constexpr int kGCpol = LGW_T * VEC * static_cast<int>(esz) >= 128 ? kCpolNT : 0;
-            const uint32_t span = static_cast<uint32_t>(ns) * rowFb;
-            const __amdgpu_buffer_rsrc_t grs = make_rsrc(
-                static_cast<const char *>(a.g) + (sub * F + f0) * static_cast<int64_t>(D) * esz, span);
-            // idle lanes: an offset past every span
-            const uint32_t laneoff = c_ok ? static_cast<uint32_t>(lc) * VEC * esz : 0x80000000u;
-            // epilogue inputs of a row (sample s, local feature fl): its mask
-            // word (the one holding this lane's columns) and x; rows past a
-            // piece's end (sample NT) read zeros
-            const int MW = a.MW;
-            const int64_t row0 = sub * F + f0;
-            const __amdgpu_buffer_rsrc_t mrs =
-                make_rsrc(kRelu ? static_cast<const void *>(a.mask + row0 * MW) : a.g,
-                          kRelu ? static_cast<uint32_t>(ns) * F * MW * 4 : 0u);
-            const __amdgpu_buffer_rsrc_t xrs =
-                make_rsrc(kLin ? static_cast<const void *>(a.x + row0) : a.g, kLin ? static_cast<uint32_t>(ns) * F * 4 : 0u);
-            const uint32_t rowMb = static_cast<uint32_t>(F) * MW * 4;
-            const uint32_t m_word_off = static_cast<uint32_t>((lcx * VEC) >> 5) * 4;
-            const int m_shift = (lcx * VEC) & 31;
-
-            // Piece t of the run: its entry, its rows' descriptors, and loads
-            // of their gradient rows.  Past j1 the piece is empty (all rows
-            // read zeros).  Every lane loads, with no branch around the load,
-            // so each piece has one counted wait.
-            auto issue = [&](int tt, float (&gv)[kL][VEC], uint2 (&dv)[kL], uint32_t &pe, uint32_t (&mv)[kL],
-                             float (&xv)[kL]) __attribute__((always_inline)) {
-                const int j = j0 + tt;
-                const bool real = j < j1;
-                pe = s_piece[real ? j : 0];
-                const int rs = static_cast<int>((pe >> 16) & 0xfff);
-                const int n = real ? static_cast<int>(pe >> 28) + 1 : 0;
-                const uint32_t flp = (pe >> 12) & 0xf;
-                const uint32_t flb = __umul24(flp, Db) + laneoff;
-#pragma unroll
-                for (int i = 0; i < kL; ++i) dv[i] = s_sdesc[i < n ? rs + i : kP];
-                // (the 24-bit products ignore the feature bits of .y)
-#pragma unroll
-                for (int i = 0; i < kL; ++i) load_grad_buf<GD, VEC, kGCpol>(grs, __umul24(dv[i].y, rowFb) + flb, gv[i]);
-                if constexpr (kRelu) {
-#pragma unroll
-                    for (int i = 0; i < kL; ++i)
-                        mv[i] = __builtin_amdgcn_raw_buffer_load_b32(
-                            mrs, __umul24(dv[i].y, rowMb) + flp * static_cast<uint32_t>(MW) * 4 + m_word_off, 0, 0);
-                }
-                if constexpr (kLin) {
-#pragma unroll
-                    for (int i = 0; i < kL; ++i)
-                        xv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                            xrs, __umul24(dv[i].y, static_cast<uint32_t>(F) * 4) + flp * 4, 0, 0));
-                }
-            };
-
-            // weight rows k and k-1 and their inverse widths for the current
-            // key, reloaded from LDS when the key changes (idle lanes read
-            // column 0; their g is 0); row k-1 serves rows with x on e_k
-            float wk[VEC], wp[VEC], lw[VEC];
-            float iwk = 0.0f, iwp = 0.0f;
-#pragma unroll
-            for (int q = 0; q < VEC; ++q) wk[q] = wp[q] = lw[q] = 0.0f;
-            auto process = [&](int tt, const float (&gv)[kL][VEC], const uint2 (&dsc)[kL], uint32_t pe,
-                               const uint32_t (&mv)[kL], const float (&xv)[kL]) __attribute__((always_inline)) {
-                const bool real = j0 + tt < j1;
-                const int n = real ? static_cast<int>(pe >> 28) + 1 : 0;
-                const int key = real ? static_cast<int>(pe & 0xffff) : cur;
-                const int fl = key >> 12;
-                if (key != cur) {
-                    flush_key();
-#pragma unroll
-                    for (int q = 0; q < VEC; ++q) ab[q] = aw[q] = 0.0f;
-                    if constexpr (kRawDb) {
-                        if (fl != db_fl) {
-                            flush_fl();
-#pragma unroll
-                            for (int q = 0; q < VEC; ++q) ad[q] = ax[q] = 0.0f;
-                            db_fl = fl;
-                        }
-                    }
-                    if constexpr (kLin) lds_load_vec<VEC>(s_lw + __umul24(fl, D) + lcx * VEC, lw);
-                    cur = key;
-                    const int k = key & 0xfff;
-                    const int kp = k > 0 ? k - 1 : 0;
-                    const int rowbase = __umul24(fl, B);
-                    lds_load_vec<VEC>(s_qw + __umul24(rowbase + k, D) + lcx * VEC, wk);
-                    lds_load_vec<VEC>(s_qw + __umul24(rowbase + kp, D) + lcx * VEC, wp);
-                    iwk = s_iw[rowbase + k];
-                    iwp = s_iw[rowbase + kp];
-                }
-                float parts[kL];
-#pragma unroll
-                for (int i = 0; i < kL; ++i) {
-                    const float qf = __uint_as_float(dsc[i].x);
-                    float gq[VEC], gm[VEC];
-                    float dot = 0.0f, dot2 = 0.0f, dotl = 0.0f;
-#pragma unroll
-                    for (int q = 0; q < VEC; ++q) {
-                        // ReLU: the forward's pass bit of column lc * VEC + q
-                        gm[q] = gv[i][q];
-                        if constexpr (kRelu)
-                            gm[q] = __uint_as_float(__float_as_uint(gm[q]) &
-                                                    static_cast<uint32_t>(__builtin_amdgcn_sbfe(
-                                                        static_cast<int>(mv[i]), m_shift + q, 1)));
-                        gq[q] = quant<Q>(gm[q]);
-                        ab[q] += gq[q];
-                        aw[q] = fmaf(qf, gq[q], aw[q]);
-                        if constexpr (kRawDb) ad[q] += kLin ? gv[i][q] : gm[q];
-                        if constexpr (kLin) {
-                            ax[q] = fmaf(gv[i][q], xv[i], ax[q]);
-                            dotl = fmaf(gv[i][q], lw[q], dotl);
-                        }
-                        dot = fmaf(gq[q], wk[q], dot);
-                        dot2 = fmaf(gq[q], wp[q], dot2);
-                    }
-                    float part = dot * iwk;
-                    if constexpr (kLin) part += dotl;
-                    // x on the bin's left edge (k >= 1): the lower bin's term too
-                    parts[i] = dsc[i].x == 0x80000000u ? fmaf(dot2, iwp, part) : part;
-                }
-                // dx into LDS by sorted row (rows past the piece's end: the
-                // discard slot)
-                if constexpr (LGW_T >= 4 && LGW_T <= 16) {
-                    // reduce-scatter: each lane ends with one row's sum
-                    static_assert(kL == 4, "four rows per piece");
-                    constexpr int kLog = LGW_T == 4 ? 2 : (LGW_T == 8 ? 3 : 4);
-                    const int r = (((lc >> (kLog - 1)) & 1) << 1) | ((lc >> (kLog - 2)) & 1);
-                    // (selects on named values: indexing the descriptor array
-                    // with r would put it in scratch memory)
-                    const uint32_t y0 = dsc[0].y, y1 = dsc[1].y, y2 = dsc[2].y, y3 = dsc[3].y;
-                    const uint32_t yr = (r & 2) ? ((r & 1) ? y3 : y2) : ((r & 1) ? y1 : y0);
-                    s_dx[r < n ? dx_slot(yr) : kP] = group_reduce_scatter4<LGW_T>(parts, lc);
-                } else {
-#pragma unroll
-                    for (int i = 0; i < kL; ++i) {
-                        float v = parts[i];
-                        if constexpr (LGW_T > 0) v = group_sum<LGW_T>(v);
-                        else v = group_sum_rt(v, lgw);
-                        s_dx[i < n ? dx_slot(dsc[i].y) : kP] = v;
-                    }
-                }
-            };
-
-            // Two register buffers: piece t+1 is in flight while piece t is
-            // reduced.  m is the same for every run, so the loop is uniform;
-            // a piece issued past m is empty.
-            float gA[kL][VEC], gB[kL][VEC];
-            uint2 dA[kL], dB[kL];
-            uint32_t pA = 0, pB = 0;
-            uint32_t mA[kL], mB[kL];     // (epilogue with ReLU)
-            float xA[kL], xB[kL];        // (epilogue with linear0)
-            if (m > 0) {
-                issue(0, gA, dA, pA, mA, xA);
-                int tt = 0;
-#pragma unroll 1
-                for (; tt + 1 < m; tt += 2) {
-                    issue(tt + 1, gB, dB, pB, mB, xB);
-                    process(tt, gA, dA, pA, mA, xA);
-                    issue(tt + 2, gA, dA, pA, mA, xA);
-                    process(tt + 1, gB, dB, pB, mB, xB);
-                }
-                if (tt < m) process(tt, gA, dA, pA, mA, xA);
-            }
-            flush_key();
-            if constexpr (kRawDb) flush_fl();
+        for (int q = 0; q < VEC; ++q) ab[q] = aw[q] = ad[q] = ax[q] = 0.0f;
+        if (lc == 0) {
+            s_rkey[lg] = -1;
+            s_rfl[lg] = -1;
         }
+        if (m > 0) {
+            int tt = 0;
+#pragma unroll 1
+            for (; tt + 1 < m; tt += 2) {
+                issue(tt + 1, gB, dB, pB, mB, xB);
+                process(tt, gA, dA, pA, mA, xA);
+                issue(tt + 2, gA, dA, pA, mA, xA);   // (unconditional: one block per step schedules better)
+                process(tt + 1, gB, dB, pB, mB, xB);
+            }
+            if (tt < m) process(tt, gA, dA, pA, mA, xA);
+        }
+        flush_key();
+        if constexpr (kRawDb) flush_fl();
+        // the next sub-tile into the other buffer (its contents, two
+        // sub-tiles back, were last read before the previous barrier)
+        const bool more = t + 1 < t_end;
+        if (dbuf && more) stash(b ^ 1);
         __syncthreads();
+        const int64_t h_sub = sub;
+        const int h_ns = ns;
+        if (dbuf && more) begin_tile(t + 1, b ^ 1);
 
         // H. dx of the sub-tile, feature-major: coalesced stores
         if (a.dxt) {
@@ -675,7 +710,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
                 const int p = tid + u * kBlock;
                 const int fl = p >> nt_shift;
                 const int sidx = p & (NT - 1);
-                if (fl < nfh && sidx < ns) a.dxt[static_cast<int64_t>(f0 + fl) * a.N + sub + sidx] = s_dx[p];
+                if (fl < nfh && sidx < h_ns) a.dxt[static_cast<int64_t>(f0 + fl) * a.N + h_sub + sidx] = s_dx[p];
             }
         }
 
@@ -721,8 +756,12 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
                 }
             }
         }
-        // (the next iteration's barrier orders these histogram updates before
-        // its pieces)
+        // (with one buffer, F is over everywhere: its descriptors can go)
+        if (!dbuf && more) stash(0);
+        // this barrier orders the dx reads before the next sub-tile's s_dx
+        // writes, and the histogram updates before its pieces
+        __syncthreads();
+        if (!dbuf && more) begin_tile(t + 1, 0);
     }
 #undef PLE_PREFETCH
     __syncthreads();
@@ -1105,16 +1144,18 @@ size_t sort_layout(BwdArgs &g, int FS, int B, int PM) {
 
 // raw_db: records carry the raw-gradient bias sums too (quantised gradients,
 // linear0 epilogue); lin: and the linear0 weight sums
-size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_db, bool lin) {
+// bufs: LDS buffers for the sub-tile descriptors, pieces and piece count
+// (two: the next sub-tile is staged while the current one is reduced)
+size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_db, bool lin, int bufs = 1) {
     LdsTaker take;
     take(g.ro_qw, 4ull * FS * B * D);
     take(g.ro_hist, 8ull * FS * B * D);
     take(g.ro_db, 4ull * FS * D);
     take(g.ro_iw, 4ull * FS * B);
     take(g.ro_nb, 4ull * FS);
-    take(g.ro_desc, 8ull * (kP + 1));
-    take(g.ro_piece, 4ull * PM);
-    take(g.ro_npc, 4);
+    take(g.ro_desc, bufs * 8ull * (kP + 1));
+    take(g.ro_piece, bufs * 4ull * PM);
+    take(g.ro_npc, bufs * 4ull);
     take(g.ro_rec, (8ull + (raw_db ? 4ull : 0ull) + (lin ? 4ull : 0ull)) * LG * D);
     take(g.ro_rkey, 4ull * LG);
     take(g.ro_rfl, 4ull * LG);
@@ -1172,6 +1213,22 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
             }
             if (best_fs > 0) {
                 const int PM = pm_for(best_fs);
+                // Two descriptor buffers when two workgroups still fit a CU
+                // with them (c1: -7 us; where they would cost a resident
+                // workgroup, as at c3, they cost more than they save, and at
+                // one workgroup per CU, as at c2, they did not pay either).
+                {
+                    BwdArgs t2 = geo;
+                    const size_t lds2 = reduce_layout(t2, best_fs, static_cast<int>(B), static_cast<int>(D), LG, PM,
+                                                      raw_db, lin, 2);
+                    const int dbuf_env = env_int("PLE_BWD_DBUF", -1);
+                    const bool dbuf = dbuf_env >= 0 ? (dbuf_env > 0 && lds2 <= kLdsMax) : (kLdsMax / lds2 >= 2);
+                    if (dbuf) {
+                        geo = t2;
+                        best_lds = lds2;
+                    }
+                    geo.dbuf = dbuf ? 1 : 0;
+                }
                 const size_t slds = sort_layout(geo, best_fs, static_cast<int>(B), PM);
                 if (slds <= kLdsMax) {
                     pl.sorted = true;
