@@ -93,7 +93,7 @@ struct BwdArgs {
     int dbuf;              // reduce: two LDS buffers for the sub-tile descriptors
     // sorted path
     int FS, G, NT, T, SPC, PM, LGW, nbits;   // T sub-tiles, SPC sub-tiles per chunk, PM piece capacity
-    int so_nb, so_edge, so_iw, so_info, so_rank, so_cnt, so_seg, so_tmp, so_desc, so_piece;   // sort LDS
+    int so_nb, so_edge, so_iw, so_cnt, so_seg, so_tmp, so_desc, so_piece;   // sort LDS
     int ro_qw, ro_hist, ro_db, ro_iw, ro_nb, ro_desc, ro_piece, ro_npc, ro_rec, ro_rkey, ro_rfl, ro_dx,
         ro_lw, ro_dlw;   // reduce LDS
 };
@@ -128,7 +128,7 @@ __device__ void block_exclusive_scan(int *a, int n, int *tmp) {
 
 constexpr int kP = 1024;                        // (sample, feature) pairs per sub-tile
 constexpr int kPairsPerThread = kP / kBlock;
-constexpr int kMaxBlocksPerFeature = kP / kWave;
+constexpr int kMaxBlocksPerFeature = kP / kWave;   // 64-pair blocks per sub-tile (a multiple of 8)
 // Rows per piece: every (feature, bin) run of a sorted sub-tile is cut into
 // pieces of kL consecutive rows (the last one shorter).
 constexpr int kL = 4;
@@ -152,9 +152,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_sort_kernel(BwdArgs a) {
     int *s_nb = reinterpret_cast<int *>(lds + a.so_nb);                 // [FS]
     float *s_edge = reinterpret_cast<float *>(lds + a.so_edge);         // [FS][B+1]
     float *s_iw = reinterpret_cast<float *>(lds + a.so_iw);             // [FS][B]
-    float2 *s_info = reinterpret_cast<float2 *>(lds + a.so_info);       // [P] {q(frac), key|edge}
-    uint8_t *s_rank = reinterpret_cast<uint8_t *>(lds + a.so_rank);     // [P]
-    uint16_t *s_cnt = reinterpret_cast<uint16_t *>(lds + a.so_cnt);     // [P/64][B+1]
+    uint16_t *s_cnt = reinterpret_cast<uint16_t *>(lds + a.so_cnt);     // [P/64][FS*(B+1)]
     int *s_seg = reinterpret_cast<int *>(lds + a.so_seg);               // [FS*(B+1)] {start | first piece << 16}
     int *s_tmp = reinterpret_cast<int *>(lds + a.so_tmp);               // [kWavesPerBlock]
     uint2 *s_sdesc = reinterpret_cast<uint2 *>(lds + a.so_desc);        // [P]
@@ -167,23 +165,25 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_sort_kernel(BwdArgs a) {
     const int64_t sub = static_cast<int64_t>(t) * NT;
     const int ns = static_cast<int>(min(static_cast<int64_t>(NT), a.N - sub));
     const int tid = threadIdx.x;
-    const int wave = tid / kWave;
     const int lane = tid % kWave;
-    const int NB = kP / kWave;                    // 64-pair blocks per sub-tile
-    const int NBf = NT / kWave;                   // blocks per feature
 
-    // pair inputs: thread -> pairs i = tid + u * kBlock, i -> (sample i / FS,
-    // feature i % FS); unconditional loads (pair 0 stands in for padding)
-    // FS and NT are powers of two: shifts instead of integer divisions
+    // Pairs in sample-major order, p = s * FS + fl (FS and NT are powers of
+    // two: shifts instead of divisions), so a wave's loads of x and the bin
+    // indices cover whole runs of each sample's features.  Thread tid holds
+    // pairs p = tid + u * kBlock: each wave's lanes hold a 64-pair block and
+    // rank it among themselves without going through LDS.  Keys are
+    // fl * KB + bin (bin B marks padding).  Unconditional loads (pair 0
+    // stands in for padding).
     const int fs_shift = __ffs(FS) - 1;
-    const int nt_shift = __ffs(NT) - 1;
+    const int NK = FS * KB;                           // keys of the sub-tile
+    const int kbits = 32 - __clz(NK - 1);             // bits of a key (NK >= 2)
     int pk[kPairsPerThread];
     float pv[kPairsPerThread];
 #pragma unroll
     for (int u = 0; u < kPairsPerThread; ++u) {
-        const int i = tid + u * kBlock;
-        const int s = i >> fs_shift;
-        const int fl = i & (FS - 1);
+        const int p = tid + u * kBlock;
+        const int s = p >> fs_shift;
+        const int fl = p & (FS - 1);
         const int64_t pair = (s < ns && fl < nfh) ? (sub + s) * F + f0 + fl : 0;
         pk[u] = load_idx<IdxT>(a.idx, pair);
         pv[u] = a.x[pair];
@@ -194,90 +194,94 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_sort_kernel(BwdArgs a) {
         s_edge[i] = i < nfh * KB ? a.edges[static_cast<int64_t>(f0) * KB + i] : 0.0f;
     for (int i = tid; i < FS * B; i += kBlock)
         s_iw[i] = i < nfh * B ? a.iw[static_cast<int64_t>(f0) * B + i] : 0.0f;
-    for (int i = tid; i < NB * KB; i += kBlock) s_cnt[i] = 0;
+    for (int i = tid; i < (kP / kWave) * NK; i += kBlock) s_cnt[i] = 0;
     __syncthreads();
 
-    // A. pair info, stored feature-major (p = fl * NT + s)
+    // A. per pair: key, edge flag, q(frac); its rank among the equal keys of
+    //    its block from 64-bit ballots (the wave64 "match-any"); the block's
+    //    first pair of each key writes the key's count
+    int pkey[kPairsPerThread];      // key | edge << 16
+    uint32_t pq[kPairsPerThread];
+    int prank[kPairsPerThread];
+    const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
 #pragma unroll
     for (int u = 0; u < kPairsPerThread; ++u) {
-        const int i = tid + u * kBlock;
-        const int s = i >> fs_shift;
-        const int fl = i & (FS - 1);
-        int key = B;
+        const int p = tid + u * kBlock;
+        const int s = p >> fs_shift;
+        const int fl = p & (FS - 1);
+        int k = B, edge = 0;
         float qf = 0.0f;
         if (s < ns && fl < nfh) {
-            const int k = clamp_bin(pk[u], s_nb[fl]);
+            k = clamp_bin(pk[u], s_nb[fl]);
             const float v = pv[u];
             const float e = s_edge[fl * KB + k];
             qf = quant<Q>((v - e) * s_iw[fl * B + k]);
-            key = k | ((k > 0 && v == e) ? 0x8000 : 0);
+            edge = k > 0 && v == e;
         }
-        s_info[(fl << nt_shift) + s] = make_float2(qf, __int_as_float(key));
-    }
-    __syncthreads();
-
-    // B. rank of each pair among equal keys of its 64-pair block
-    for (int b = wave; b < NB; b += kWavesPerBlock) {
-        const int p = b * kWave + lane;
-        const int k = __float_as_int(s_info[p].y) & 0x7fff;
+        const int key = fl * KB + k;
+        pkey[u] = key | (edge << 16);
+        pq[u] = __float_as_uint(qf);
         unsigned long long m = ~0ull;
-        for (int bit = 0; bit < a.nbits; ++bit) {
-            const bool set = (k >> bit) & 1;
+        for (int bit = 0; bit < kbits; ++bit) {
+            const bool set = (key >> bit) & 1;
             const unsigned long long bal = __ballot(set);
             m &= set ? bal : ~bal;
         }
-        const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
         const int rank = __popcll(m & lt);
-        s_rank[p] = static_cast<uint8_t>(rank);
-        if (rank == 0) s_cnt[b * KB + k] = static_cast<uint16_t>(__popcll(m));
+        prank[u] = rank;
+        if (rank == 0) s_cnt[(p / kWave) * NK + key] = static_cast<uint16_t>(__popcll(m));
     }
     __syncthreads();
 
-    // C. per key: exclusive prefix of its counts over the feature's blocks
-    //    (held in registers), then {count | pieces << 16} for the scan
-    for (int kk = tid; kk < FS * KB; kk += kBlock) {
-        // fl = kk / KB without a division (FS <= 16)
-        int fl = 0;
-        while (fl + 1 < FS && kk >= (fl + 1) * KB) ++fl;
-        const int k = kk - fl * KB;
-        uint16_t *col = s_cnt + fl * NBf * KB + k;
-        int cc[kMaxBlocksPerFeature];
-#pragma unroll
-        for (int bb = 0; bb < kMaxBlocksPerFeature; ++bb) cc[bb] = bb < NBf ? col[bb * KB] : 0;
+    // C. per key: exclusive prefix of its counts over the blocks (held in
+    //    registers), then {count | pieces << 16} for the scan
+    for (int kk = tid; kk < NK; kk += kBlock) {
+        uint16_t *col = s_cnt + kk;
         int run = 0;
+        // eight blocks' counts in flight at a time (registers)
+        for (int b0 = 0; b0 < kMaxBlocksPerFeature; b0 += 8) {
+            int cc[8];
 #pragma unroll
-        for (int bb = 0; bb < kMaxBlocksPerFeature; ++bb) {
-            if (bb < NBf) col[bb * KB] = static_cast<uint16_t>(run);
-            run += cc[bb];
+            for (int bb = 0; bb < 8; ++bb) cc[bb] = col[(b0 + bb) * NK];
+#pragma unroll
+            for (int bb = 0; bb < 8; ++bb) {
+                col[(b0 + bb) * NK] = static_cast<uint16_t>(run);
+                run += cc[bb];
+            }
         }
-        const int pieces = k < B ? (run + kL - 1) / kL : 0;   // padding rows (key B): none
+        // padding rows (bin B of a feature): no pieces.  (kk % KB without a
+        // division: FS <= 16)
+        int k = kk;
+        while (k >= KB) k -= KB;
+        const int pieces = k < B ? (run + kL - 1) / kL : 0;
         s_seg[kk] = run | (pieces << 16);
     }
     __syncthreads();
     // run starts (low half) and first piece of each run (high half); neither
     // sum reaches 2^16
-    block_exclusive_scan(s_seg, FS * KB, s_tmp);
+    block_exclusive_scan(s_seg, NK, s_tmp);
 
     // D. scatter: sorted position -> row descriptor; the first row of every
     //    piece writes the piece's entry
-    for (int p = tid; p < kP; p += kBlock) {
-        const int fl = p >> nt_shift;
-        const int s = p & (NT - 1);
-        const float2 inf = s_info[p];
-        const int kb = __float_as_int(inf.y);
-        const int k = kb & 0x7fff;
-        const int sg = s_seg[fl * KB + k];
-        const int within = s_cnt[(p / kWave) * KB + k] + s_rank[p];
+#pragma unroll
+    for (int u = 0; u < kPairsPerThread; ++u) {
+        const int p = tid + u * kBlock;
+        const int s = p >> fs_shift;
+        const int fl = p & (FS - 1);
+        const int key = pkey[u] & 0xffff;
+        const int k = key - fl * KB;
+        const int sg = s_seg[key];
+        const int within = s_cnt[(p / kWave) * NK + key] + prank[u];
         const int slot = (sg & 0xffff) + within;
         // x on e_k (k >= 1) gives q(frac) == +0 exactly; such rows carry -0
         // instead, which marks the edge term and adds the same zero.  A -0
         // from anywhere else becomes +0 (the same contribution).
-        uint32_t qbits = __float_as_uint(inf.x);
-        qbits = (kb & 0x8000) ? 0x80000000u : (qbits == 0x80000000u ? 0u : qbits);
+        uint32_t qbits = pq[u];
+        qbits = (pkey[u] >> 16) ? 0x80000000u : (qbits == 0x80000000u ? 0u : qbits);
         s_sdesc[slot] = make_uint2(qbits, static_cast<uint32_t>(s) | (static_cast<uint32_t>(fl) << 24));
         if (k < B && within % kL == 0) {
             // the run ends where the next key's (at least the padding key B) begins
-            const int end = s_seg[fl * KB + k + 1] & 0xffff;
+            const int end = s_seg[key + 1] & 0xffff;
             const int rows = min(kL, end - slot);
             s_piece[(sg >> 16) + within / kL] = static_cast<uint32_t>(k) | (static_cast<uint32_t>(fl) << 12) |
                                                 (static_cast<uint32_t>(slot) << 16) |
@@ -1132,9 +1136,7 @@ size_t sort_layout(BwdArgs &g, int FS, int B, int PM) {
     take(g.so_nb, 4ull * FS);
     take(g.so_edge, 4ull * FS * KB);
     take(g.so_iw, 4ull * FS * B);
-    take(g.so_info, 8ull * kP);
-    take(g.so_rank, 1ull * kP);
-    take(g.so_cnt, 2ull * (kP / kWave) * KB);
+    take(g.so_cnt, 2ull * (kP / kWave) * FS * KB);
     take(g.so_seg, 4ull * (FS * KB + 1));
     take(g.so_tmp, 4ull * kWavesPerBlock);
     take(g.so_desc, 8ull * kP);
