@@ -249,6 +249,8 @@ def _random_case(n, f, bmax, d, seed, ragged=True):
 SHAPES = [
     (1, 1, 1, 1), (7, 3, 5, 10), (129, 5, 7, 15), (1000, 9, 48, 20), (333, 1, 300, 16),
     (2500, 17, 64, 64), (513, 6, 256, 24), (64, 33, 2, 3), (1025, 4, 130, 2), (700, 2, 1000, 8),
+    # finalize without an LDS table (B * 2 * 8 * 4 bytes > 160 KiB) over several chunks summed first
+    (3000, 2, 3000, 4),
 ]
 
 
@@ -269,6 +271,27 @@ def test_shape_sweep_forward_and_backward(shape, c_oracle):
     gx2, _, _ = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, True, False, False)
     _, gw2, gb2 = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, False, True, True)
     assert torch.equal(gx, gx2) and torch.equal(gw, gw2) and torch.equal(gb, gb2)
+
+
+@pytest.mark.parametrize("cfg", [1, 3])
+def test_backward_descriptor_buffering_modes_agree(cfg, c_oracle, monkeypatch):
+    """One or two LDS buffers for the sorted descriptors (the planner picks by
+    LDS room; PLE_BWD_DBUF forces either): same pieces, same order of every
+    sum, so bitwise the same gradients, both checked against the oracle."""
+    w = workloads.make(cfg, REDUCED[cfg])
+    n, f, bmax, d = w.shape
+    print(f"buffering modes {w.name} shape={w.shape}", flush=True)
+    x, e, iw, nb, wt, bt = _inputs(w)
+    _, idx = ops.forward_with_bias(x, e, iw, nb, wt, bt, torch.float32)
+    g = _grad((n, f, d), 11)
+    res = []
+    for mode in ("0", "1"):
+        monkeypatch.setenv("PLE_BWD_DBUF", mode)
+        res.append(ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, True, True, True))
+    monkeypatch.delenv("PLE_BWD_DBUF")
+    for a_, b_ in zip(*res):
+        assert torch.equal(a_, b_)
+    _check_backward(w, "f32", g, *res[1], c_oracle)
 
 
 @pytest.mark.parametrize("cfg", [0, 1, 2, 3])
