@@ -134,9 +134,12 @@ constexpr int kMaxBlocksPerFeature = kP / kWave;   // 64-pair blocks per sub-til
 constexpr int kL = 4;
 // Piece capacity per sub-tile: at most P / kL + (non-empty keys) pieces.
 constexpr int kMaxPieces = kP / kL + kP;
-constexpr int kPieceRegs = (kMaxPieces + kBlock - 1) / kBlock;
 
 // backward epilogue flags (template argument of the reduce kernel)
+// Reduce workgroups of twice the usual size: where LDS leaves room for only
+// one reduce workgroup per CU, its waves are all the CU has to hide latency.
+constexpr int kWideBlock = 2 * kBlock;
+
 constexpr int kBwdRelu = 1;
 constexpr int kBwdLin = 2;
 
@@ -305,8 +308,8 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_sort_kernel(BwdArgs a) {
 // reduce
 // ---------------------------------------------------------------------------
 
-template <int GD, int Q, int VEC, int LGW_T, int EPI>
-__global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
+template <int GD, int Q, int VEC, int LGW_T, int EPI, int RB>
+__global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
     constexpr bool kRelu = (EPI & kBwdRelu) != 0;
     constexpr bool kLin = (EPI & kBwdLin) != 0;
     // With fp32 rounding and no linear0 branch the bias gradient is the sum of
@@ -341,25 +344,30 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
     const int PM = a.PM;
 
     // The next sub-tile's descriptors, pieces and piece count travel in
-    // registers while the current one is reduced (kP / 2 / kBlock == 2 uint4
-    // of descriptors per thread; kPieceRegs piece entries, the ones past the
+    // registers while the current one is reduced (kP / 2 / RB uint4 of
+    // descriptors per thread; kPieceRegsRB piece entries, the ones past the
     // capacity re-read entry 0 and are never stored).
-    static_assert(kP / 2 / kBlock == 2 && kPieceRegs == 5, "prefetch registers");
-    uint4 pd0, pd1;
-    uint32_t pp0, pp1, pp2, pp3, pp4;
+    // (named registers, not arrays: a loop over a register array that is not
+    // unrolled would put it in scratch memory)
+    constexpr int kDescRegs = kP / 2 / RB;
+    constexpr int kPieceRegsRB = (kMaxPieces + RB - 1) / RB;
+    static_assert(kDescRegs * 2 * RB == kP && kDescRegs <= 2 && kPieceRegsRB >= 3 && kPieceRegsRB <= 5,
+                  "prefetch registers");
+    uint4 pd0, pd1 = make_uint4(0u, 0u, 0u, 0u);
+    uint32_t pp0, pp1, pp2, pp3 = 0, pp4 = 0;
     int pnpc;
 #define PLE_PREFETCH(T_)                                                                         \
     do {                                                                                         \
         const int64_t tile_ = static_cast<int64_t>(T_) * a.G + g;                                \
         const uint4 *src_ = reinterpret_cast<const uint4 *>(a.desc + tile_ * kP);                \
         pd0 = src_[tid];                                                                         \
-        pd1 = src_[tid + kBlock];                                                                \
+        if constexpr (kDescRegs > 1) pd1 = src_[tid + RB];                                       \
         const uint32_t *ps_ = a.piece + tile_ * PM;                                              \
         pp0 = ps_[tid < PM ? tid : 0];                                                           \
-        pp1 = ps_[tid + kBlock < PM ? tid + kBlock : 0];                                         \
-        pp2 = ps_[tid + 2 * kBlock < PM ? tid + 2 * kBlock : 0];                                 \
-        pp3 = ps_[tid + 3 * kBlock < PM ? tid + 3 * kBlock : 0];                                 \
-        pp4 = ps_[tid + 4 * kBlock < PM ? tid + 4 * kBlock : 0];                                 \
+        pp1 = ps_[tid + RB < PM ? tid + RB : 0];                                                 \
+        pp2 = ps_[tid + 2 * RB < PM ? tid + 2 * RB : 0];                                         \
+        if constexpr (kPieceRegsRB > 3) pp3 = ps_[tid + 3 * RB < PM ? tid + 3 * RB : 0];         \
+        if constexpr (kPieceRegsRB > 4) pp4 = ps_[tid + 4 * RB < PM ? tid + 4 * RB : 0];         \
         pnpc = a.npc[tile_];                                                                     \
     } while (0)
     PLE_PREFETCH(t_begin);
@@ -371,21 +379,21 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
         s_sdesc[kP] = make_uint2(0u, static_cast<uint32_t>(NT));
         if (a.dbuf) s_sdesc[2 * kP + 1] = make_uint2(0u, static_cast<uint32_t>(NT));
     }
-    for (int i = tid; i < FS; i += kBlock) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
-    for (int i = tid; i < FS * B; i += kBlock) {
+    for (int i = tid; i < FS; i += RB) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
+    for (int i = tid; i < FS * B; i += RB) {
         const int fl = i / B;
         s_iw[i] = fl < nfh ? a.iw[static_cast<int64_t>(f0) * B + i] : 0.0f;
     }
-    for (int i = tid; i < FS * B * 2 * D; i += kBlock) s_hist[i] = 0.0f;
-    for (int i = tid; i < FS * D; i += kBlock) s_db[i] = 0.0f;
+    for (int i = tid; i < FS * B * 2 * D; i += RB) s_hist[i] = 0.0f;
+    for (int i = tid; i < FS * D; i += RB) s_db[i] = 0.0f;
     if constexpr (kLin) {
-        for (int i = tid; i < FS * D; i += kBlock) {
+        for (int i = tid; i < FS * D; i += RB) {
             s_lw[i] = i / D < nfh ? a.lin_w[static_cast<int64_t>(f0) * D + i] : 0.0f;
             s_dlw[i] = 0.0f;
         }
     }
     __syncthreads();
-    for (int i = tid; i < FS * B * D; i += kBlock) {
+    for (int i = tid; i < FS * B * D; i += RB) {
         const int fl = i / (B * D);
         const int r = i - fl * (B * D);
         const int k = r / D;
@@ -399,7 +407,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
     }
 
     const int lgw = LGW_T > 0 ? LGW_T : a.LGW;   // lanes per grad_output row (power of two)
-    const int LG = kBlock / lgw;                  // lane groups (runs of pieces) per workgroup
+    const int LG = RB / lgw;                  // lane groups (runs of pieces) per workgroup
     const int lg = tid / lgw;
     const int lc = tid - lg * lgw;
     const bool c_ok = lc < D / VEC;
@@ -518,14 +526,18 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
     // prefetch registers into LDS buffer b
     auto stash = [&](int b) __attribute__((always_inline)) {
         uint2 *dd = s_sdesc + b * (kP + 1);
-        uint32_t *pp = s_piece + b * PM;
+        uint32_t *ps = s_piece + b * PM;
         reinterpret_cast<uint4 *>(dd)[tid] = pd0;
-        reinterpret_cast<uint4 *>(dd)[tid + kBlock] = pd1;
-        if (tid < PM) pp[tid] = pp0;
-        if (tid + kBlock < PM) pp[tid + kBlock] = pp1;
-        if (tid + 2 * kBlock < PM) pp[tid + 2 * kBlock] = pp2;
-        if (tid + 3 * kBlock < PM) pp[tid + 3 * kBlock] = pp3;
-        if (tid + 4 * kBlock < PM) pp[tid + 4 * kBlock] = pp4;
+        if constexpr (kDescRegs > 1) reinterpret_cast<uint4 *>(dd)[tid + RB] = pd1;
+        if (tid < PM) ps[tid] = pp0;
+        if (tid + RB < PM) ps[tid + RB] = pp1;
+        if (tid + 2 * RB < PM) ps[tid + 2 * RB] = pp2;
+        if constexpr (kPieceRegsRB > 3) {
+            if (tid + 3 * RB < PM) ps[tid + 3 * RB] = pp3;
+        }
+        if constexpr (kPieceRegsRB > 4) {
+            if (tid + 4 * RB < PM) ps[tid + 4 * RB] = pp4;
+        }
         if (tid == 0) s_npc[b] = pnpc;
     };
 
@@ -710,8 +722,8 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
         // H. dx of the sub-tile, feature-major: coalesced stores
         if (a.dxt) {
 #pragma unroll
-            for (int u = 0; u < kPairsPerThread; ++u) {
-                const int p = tid + u * kBlock;
+            for (int u = 0; u < (kP / RB); ++u) {
+                const int p = tid + u * RB;
                 const int fl = p >> nt_shift;
                 const int sidx = p & (NT - 1);
                 if (fl < nfh && sidx < h_ns) a.dxt[static_cast<int64_t>(f0 + fl) * a.N + h_sub + sidx] = s_dx[p];
@@ -773,19 +785,19 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_reduce_kernel(BwdArgs a) {
     // chunk partials
     if (a.part) {
         float *dst = a.part + (static_cast<int64_t>(c) * F + f0) * B * D2;
-        for (int i = tid; i < FS * B * D2; i += kBlock) {
+        for (int i = tid; i < FS * B * D2; i += RB) {
             const int fl = i / (B * D2);
             const int k = (i - fl * B * D2) / D2;
             if (fl < nfh && k < s_nb[fl]) dst[i] = s_hist[i];
         }
         if constexpr (kRawDb) {
             float *dstb = a.part_db + (static_cast<int64_t>(c) * F + f0) * D;
-            for (int i = tid; i < FS * D; i += kBlock)
+            for (int i = tid; i < FS * D; i += RB)
                 if (i / D < nfh) dstb[i] = s_db[i];
         }
         if constexpr (kLin) {
             float *dstl = a.part_lw + (static_cast<int64_t>(c) * F + f0) * D;
-            for (int i = tid; i < FS * D; i += kBlock)
+            for (int i = tid; i < FS * D; i += RB)
                 if (i / D < nfh) dstl[i] = s_dlw[i];
         }
     }
@@ -1110,6 +1122,7 @@ int env_int(const char *name, int dflt) {
 struct BwdPlan {
     bool sorted;
     int vec;
+    int rb;          // reduce workgroup size
     int C, Cd;
     int64_t NC;
     size_t lds, sort_lds;
@@ -1170,6 +1183,7 @@ size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_
 // g_align16: the gradient's base address is 16-byte aligned
 BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16, bool raw_db, bool lin) {
     BwdPlan pl{};
+    pl.rb = kBlock;
     const int cus = device_cu_count();
     pl.sorted = false;
     // Sorted path: bins fit the 12-bit field of a piece, and a sub-tile's
@@ -1213,15 +1227,37 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                     geo = t;
                 }
             }
+            int rb = kBlock, LGc = LG;
             if (best_fs > 0) {
                 const int PM = pm_for(best_fs);
+                // Twice the workgroup size where LDS leaves room for one
+                // reduce workgroup per CU (fp32 gradient and quantisation, no
+                // linear0 branch): c2 -20 us; where two fit, the wide form
+                // measured slower (c3 +28 us, c4 +190 us).
+                {
+                    const bool wide_ok = !raw_db && vec != 8;
+                    bool wide = wide_ok && kLdsMax / best_lds < 2;
+                    const int rb_env = env_int("PLE_BWD_RB", 0);
+                    if (rb_env == kBlock || rb_env == kWideBlock) wide = wide_ok && rb_env == kWideBlock;
+                    if (wide) {
+                        BwdArgs tw = geo;
+                        const size_t ldsw = reduce_layout(tw, best_fs, static_cast<int>(B), static_cast<int>(D),
+                                                          kWideBlock / lgw, PM, raw_db, lin);
+                        if (ldsw <= kLdsMax) {
+                            geo = tw;
+                            best_lds = ldsw;
+                            rb = kWideBlock;
+                            LGc = kWideBlock / lgw;
+                        }
+                    }
+                }
                 // Two descriptor buffers when two workgroups still fit a CU
                 // with them (c1: -7 us; where they would cost a resident
                 // workgroup, as at c3, they cost more than they save, and at
                 // one workgroup per CU, as at c2, they did not pay either).
                 {
                     BwdArgs t2 = geo;
-                    const size_t lds2 = reduce_layout(t2, best_fs, static_cast<int>(B), static_cast<int>(D), LG, PM,
+                    const size_t lds2 = reduce_layout(t2, best_fs, static_cast<int>(B), static_cast<int>(D), LGc, PM,
                                                       raw_db, lin, 2);
                     const int dbuf_env = env_int("PLE_BWD_DBUF", -1);
                     const bool dbuf = dbuf_env >= 0 ? (dbuf_env > 0 && lds2 <= kLdsMax) : (kLdsMax / lds2 >= 2);
@@ -1235,6 +1271,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                 if (slds <= kLdsMax) {
                     pl.sorted = true;
                     pl.vec = vec;
+                    pl.rb = rb;
                     pl.lds = best_lds;
                     pl.sort_lds = slds;
                     geo.FS = best_fs;
@@ -1299,47 +1336,49 @@ hipError_t launch_sort(const BwdArgs &a, int idxb, dim3 grid, size_t lds, hipStr
 
 // Lane-group width as a template argument for the 8- and 4-float rows (DPP
 // reductions); the one-column-per-lane variant takes it at run time.
-template <int GD, int Q, int EPI>
+template <int GD, int Q, int EPI, int RB>
 hipError_t launch_reduce_epi(const BwdArgs &a, int vec, dim3 grid, size_t lds, hipStream_t s) {
     if (vec == 4) {
         switch (a.LGW) {
-            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 4, EPI>), grid, dim3(kBlock), lds, s, a); break;
-            case 8: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 8, EPI>), grid, dim3(kBlock), lds, s, a); break;
-            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 16, EPI>), grid, dim3(kBlock), lds, s, a); break;
+            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 4, EPI, RB>), grid, dim3(RB), lds, s, a); break;
+            case 8: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 8, EPI, RB>), grid, dim3(RB), lds, s, a); break;
+            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 16, EPI, RB>), grid, dim3(RB), lds, s, a); break;
         }
     } else {
-        hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 0, EPI>), grid, dim3(kBlock), lds, s, a);
+        hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 0, EPI, RB>), grid, dim3(RB), lds, s, a);
     }
     return hipGetLastError();
 }
 
+// rb: the reduce workgroup size, kBlock or kWideBlock (fp32 gradient and
+// quantisation, no linear0 branch; the planner picks it).
 template <int GD, int Q>
-hipError_t launch_reduce(const BwdArgs &a, int vec, int epi, dim3 grid, size_t lds, hipStream_t s) {
+hipError_t launch_reduce(const BwdArgs &a, int vec, int epi, int rb, dim3 grid, size_t lds, hipStream_t s) {
+    if (rb == kWideBlock) {
+        if constexpr (GD == PLE_DTYPE_F32 && Q == PLE_DTYPE_F32) {
+            if (vec != 8 && epi == 0) return launch_reduce_epi<GD, Q, 0, kWideBlock>(a, vec, grid, lds, s);
+            if (vec != 8 && epi == kBwdRelu) return launch_reduce_epi<GD, Q, kBwdRelu, kWideBlock>(a, vec, grid, lds, s);
+        }
+        return hipErrorInvalidConfiguration;   // (the planner never asks for it elsewhere)
+    }
     if constexpr (GD == PLE_DTYPE_F32) {
         // module epilogues (their gradient is fp32); no 8-float rows
         switch (epi) {
-            case kBwdRelu: return launch_reduce_epi<GD, Q, kBwdRelu>(a, vec, grid, lds, s);
-            case kBwdLin: return launch_reduce_epi<GD, Q, kBwdLin>(a, vec, grid, lds, s);
-            case kBwdLin | kBwdRelu: return launch_reduce_epi<GD, Q, kBwdLin | kBwdRelu>(a, vec, grid, lds, s);
+            case kBwdRelu: return launch_reduce_epi<GD, Q, kBwdRelu, kBlock>(a, vec, grid, lds, s);
+            case kBwdLin: return launch_reduce_epi<GD, Q, kBwdLin, kBlock>(a, vec, grid, lds, s);
+            case kBwdLin | kBwdRelu: return launch_reduce_epi<GD, Q, kBwdLin | kBwdRelu, kBlock>(a, vec, grid, lds, s);
             default: break;
         }
     }
     if (vec == 8) {
         switch (a.LGW) {
-            case 2: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 2, 0>), grid, dim3(kBlock), lds, s, a); break;
-            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 4, 0>), grid, dim3(kBlock), lds, s, a); break;
-            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 8, 0>), grid, dim3(kBlock), lds, s, a); break;
+            case 2: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 2, 0, kBlock>), grid, dim3(kBlock), lds, s, a); break;
+            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 4, 0, kBlock>), grid, dim3(kBlock), lds, s, a); break;
+            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 8, 0, kBlock>), grid, dim3(kBlock), lds, s, a); break;
         }
-    } else if (vec == 4) {
-        switch (a.LGW) {
-            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 4, 0>), grid, dim3(kBlock), lds, s, a); break;
-            case 8: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 8, 0>), grid, dim3(kBlock), lds, s, a); break;
-            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 16, 0>), grid, dim3(kBlock), lds, s, a); break;
-        }
-    } else {
-        hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 0, 0>), grid, dim3(kBlock), lds, s, a);
+        return hipGetLastError();
     }
-    return hipGetLastError();
+    return launch_reduce_epi<GD, Q, 0, kBlock>(a, vec, grid, lds, s);
 }
 
 template <int GD, int Q>
@@ -1350,7 +1389,8 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
         a.db_from_buckets = Q == PLE_DTYPE_F32 && a.lin_w == nullptr;
         e = launch_sort<Q>(a, idxb, dim3(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, a.T))), pl.sort_lds, s);
         if (e != hipSuccess) return e;
-        e = launch_reduce<GD, Q>(a, pl.vec, epi, dim3(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, pl.C))), pl.lds, s);
+        e = launch_reduce<GD, Q>(a, pl.vec, epi, pl.rb, dim3(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, pl.C))),
+                                 pl.lds, s);
         if (e != hipSuccess) return e;
         if (a.dxt) {
             const dim3 tg(static_cast<unsigned>((a.N + kTr - 1) / kTr), static_cast<unsigned>((a.F + kTr - 1) / kTr));
