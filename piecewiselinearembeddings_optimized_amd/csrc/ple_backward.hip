@@ -961,6 +961,9 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_chunksum_kernel(float *part, i
 // ---------------------------------------------------------------------------
 
 constexpr int kFinCols = 8;
+// LDS row stride of the chunk-sum table: one more than kFinCols, so that the
+// lanes of a column (consecutive bins) read distinct banks
+constexpr int kFinStride = kFinCols + 1;
 constexpr int kFinLoadsInline = 128;   // chunk-sum loads per finalize thread, at most
 
 // Sums the chunk partials of every (bin, column) of the group in chunk order
@@ -975,7 +978,7 @@ constexpr int kFinLoadsInline = 128;   // chunk-sum loads per finalize thread, a
 constexpr int kFinLanes = kBlock / kFinCols;   // lanes per column (half a wave)
 
 __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
-    extern __shared__ float tot[];       // [n][2][kFinCols]
+    extern __shared__ float tot[];       // [n][2][kFinStride]
     const int f = blockIdx.x;
     const int j0 = blockIdx.y * kFinCols;
     const int B = a.B, D = a.D;
@@ -990,7 +993,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
     // bin k's chunk sum of half h (0: bucket, 1: weighted) for this lane's column
     // (fin_direct implies summed chunks)
     auto total = [&](int k, int h) {
-        if (!a.fin_direct) return tot[(k * 2 + h) * kFinCols + col];
+        if (!a.fin_direct) return tot[(k * 2 + h) * kFinStride + col];
         return src[k * D2 + h * D + j0 + col];
     };
     const int nsum = a.fin_summed ? 1 : a.Cd;
@@ -1007,7 +1010,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
 #pragma unroll 8
                 for (int cc = 0; cc < nsum; ++cc) sum += p[cc * cstride];
             }
-            tot[e] = sum;
+            tot[(k * 2 + h) * kFinStride + cidx] = sum;
         }
         __syncthreads();
     }
@@ -1421,7 +1424,7 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
         }
     }
     if (want_dwdb) {
-        size_t lds = static_cast<size_t>(a.B) * 2 * kFinCols * sizeof(float);
+        size_t lds = static_cast<size_t>(a.B) * 2 * kFinStride * sizeof(float);
         a.fin_direct = lds > kLdsMax;          // very many bins: no LDS table
         if (a.fin_direct) lds = 0;
         // The finalize sums the chunks itself unless a thread would issue more
