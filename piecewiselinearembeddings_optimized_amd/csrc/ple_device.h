@@ -198,7 +198,7 @@ __device__ __forceinline__ void lds_store_vec(float *p, const float *v) {
     }
 }
 
-// Stores VEC consecutive outputs as OUT (VEC in {1, 4}), with the
+// Stores VEC consecutive outputs as OUT (VEC in {1, 4}; 8 for 16-bit OUT), with the
 // non-temporal hint: the output is written once and not read back here.
 template <int OUT, int VEC>
 __device__ __forceinline__ void store_out(void *base, int64_t i, const float *v) {
@@ -216,7 +216,14 @@ __device__ __forceinline__ void store_out(void *base, int64_t i, const float *v)
 #pragma unroll
         for (int t = 0; t < VEC; ++t) h[t] = (OUT == PLE_DTYPE_BF16) ? bf16_bits(v[t]) : f16_bits(v[t]);
         uint16_t *p = static_cast<uint16_t *>(base) + i;
-        if constexpr (VEC == 4) {
+        if constexpr (VEC == 8) {
+            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+            const u32x4 w = {static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16),
+                             static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16),
+                             static_cast<uint32_t>(h[4]) | (static_cast<uint32_t>(h[5]) << 16),
+                             static_cast<uint32_t>(h[6]) | (static_cast<uint32_t>(h[7]) << 16)};
+            __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(p));
+        } else if constexpr (VEC == 4) {
             typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
             const u32x2 w = {static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16),
                              static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16)};

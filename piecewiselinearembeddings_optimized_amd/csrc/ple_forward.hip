@@ -119,12 +119,15 @@ __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
                 const int p = phys_bin(k, n, B);
                 const float *src = a.weight + ((static_cast<int64_t>(f0 + fl) * B + p) * D + u * VEC);
                 float *dst = tbl + (static_cast<size_t>(fl) * B + k) * rs + D + u * VEC;
-                if constexpr (VEC == 4) {
-                    const float4 w = *reinterpret_cast<const float4 *>(src);
-                    dst[0] = quant<Q>(w.x);
-                    dst[1] = quant<Q>(w.y);
-                    dst[2] = quant<Q>(w.z);
-                    dst[3] = quant<Q>(w.w);
+                if constexpr (VEC % 4 == 0) {
+#pragma unroll
+                    for (int h = 0; h < VEC; h += 4) {
+                        const float4 w = *reinterpret_cast<const float4 *>(src + h);
+                        dst[h] = quant<Q>(w.x);
+                        dst[h + 1] = quant<Q>(w.y);
+                        dst[h + 2] = quant<Q>(w.z);
+                        dst[h + 3] = quant<Q>(w.w);
+                    }
                 } else {
                     dst[0] = quant<Q>(src[0]);
                 }
@@ -246,13 +249,16 @@ __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
                 const int64_t n = n0 + s;
                 const float *row = o_tbl + static_cast<size_t>(ks[q]) * rs;
                 float r[VEC];
-                if constexpr (VEC == 4) {
-                    const float4 P = *reinterpret_cast<const float4 *>(row);
-                    const float4 W = *reinterpret_cast<const float4 *>(row + D);
-                    r[0] = fmaf(qs[q], W.x, P.x);
-                    r[1] = fmaf(qs[q], W.y, P.y);
-                    r[2] = fmaf(qs[q], W.z, P.z);
-                    r[3] = fmaf(qs[q], W.w, P.w);
+                if constexpr (VEC % 4 == 0) {
+#pragma unroll
+                    for (int h = 0; h < VEC; h += 4) {
+                        const float4 P = *reinterpret_cast<const float4 *>(row + h);
+                        const float4 W = *reinterpret_cast<const float4 *>(row + D + h);
+                        r[h] = fmaf(qs[q], W.x, P.x);
+                        r[h + 1] = fmaf(qs[q], W.y, P.y);
+                        r[h + 2] = fmaf(qs[q], W.z, P.z);
+                        r[h + 3] = fmaf(qs[q], W.w, P.w);
+                    }
                 } else {
                     r[0] = fmaf(qs[q], row[D], row[0]);
                 }
@@ -319,8 +325,12 @@ struct FwdPlan {
 // PLE_FWD_FS / PLE_FWD_WG_PER_CU override the two choices (tuning).
 constexpr int kOutPerTable = 10;
 
-bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, bool aligned16, FwdPlan &pl) {
+// out16: the output's base address is 16-byte aligned (8 outputs per lane)
+bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, bool aligned16, bool out16, FwdPlan &pl) {
+    // 16-bit outputs: 8 per lane (one 16-byte store) when D allows, so a
+    // store instruction carries as many bytes as fp32's 4 per lane
     pl.vec = (D % 4 == 0 && aligned16) ? 4 : 1;
+    if (out_bytes == 2 && D % 8 == 0 && aligned16 && out16 && env_int("PLE_FWD_VEC", 0) != 4) pl.vec = 8;
     const int U = static_cast<int>(D / pl.vec);
     if (U > kWave) return false;
     const int Bi = static_cast<int>(B), Di = static_cast<int>(D);
@@ -366,6 +376,10 @@ hipError_t launch_idx(const FwdArgs &a, int idxb, dim3 grid, size_t lds, hipStre
 
 template <int Q, int OUT, int EPI>
 hipError_t launch_vec(const FwdArgs &a, int vec, int idxb, dim3 grid, size_t lds, hipStream_t s) {
+    // (8 outputs per lane: 16-bit outputs without an epilogue only)
+    if constexpr (OUT != PLE_DTYPE_F32 && EPI == kEpiNone) {
+        if (vec == 8) return launch_idx<Q, OUT, EPI, 8>(a, idxb, grid, lds, s);
+    }
     return vec == 4 ? launch_idx<Q, OUT, EPI, 4>(a, idxb, grid, lds, s)
                     : launch_idx<Q, OUT, EPI, 1>(a, idxb, grid, lds, s);
 }
@@ -398,7 +412,8 @@ int forward_run(const ForwardRequest &r) {
     const bool aligned16 = (reinterpret_cast<uintptr_t>(r.out) % (4 * out_bytes) == 0) &&
                            (reinterpret_cast<uintptr_t>(r.weight) % 16 == 0);
     FwdPlan pl;
-    if (!plan_forward(r.N, r.F, r.B, r.D, out_bytes, aligned16, pl)) return PLE_E_UNSUPPORTED;
+    if (!plan_forward(r.N, r.F, r.B, r.D, out_bytes, aligned16, reinterpret_cast<uintptr_t>(r.out) % 16 == 0, pl))
+        return PLE_E_UNSUPPORTED;
     FwdArgs a;
     a.x = r.x; a.edges = r.edges; a.iw = r.iw; a.nbins = r.nbins; a.weight = r.weight;
     a.bias = r.bias; a.lin_w = r.lin_w; a.lin_b = r.lin_b;
