@@ -107,6 +107,21 @@ def test_forward_float16_matches_oracle(cfg, c_oracle):
     assert rel <= 1e-3   # half keeps 11 significant bits
 
 
+@pytest.mark.parametrize("cfg,dtype", [(1, torch.float16), (4, torch.bfloat16)])
+def test_forward_16bit_store_widths_agree(cfg, dtype, monkeypatch):
+    """16-bit outputs store 8 per lane when D allows (16-byte stores) or 4 per
+    lane (PLE_FWD_VEC=4 forces it): the same bits either way."""
+    w = workloads.make(cfg, REDUCED[cfg])
+    print(f"forward store widths {w.name} {dtype}", flush=True)
+    x, e, iw, nb, wt, bt = _inputs(w)
+    out8, idx8 = ops.forward(x, e, iw, nb, wt, dtype)
+    monkeypatch.setenv("PLE_FWD_VEC", "4")
+    out4, idx4 = ops.forward(x, e, iw, nb, wt, dtype)
+    monkeypatch.delenv("PLE_FWD_VEC")
+    assert torch.equal(idx8, idx4)
+    assert torch.equal(out8.view(torch.int16), out4.view(torch.int16))
+
+
 @pytest.mark.parametrize("cfg", [0, 1, 2])
 def test_backward_float16_grad_matches_oracle(cfg, c_oracle):
     """fp16 gradient with fp16 quantisation (the backward of the autocast-fp16
