@@ -499,6 +499,15 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
     const uint32_t rowMb = static_cast<uint32_t>(F) * MW * 4;
     const uint32_t m_word_off = static_cast<uint32_t>((lcx * VEC) >> 5) * 4;
     const int m_shift = (lcx * VEC) & 31;
+    // Lane groups of four or more lanes fetch a piece's epilogue inputs once
+    // per quad of lanes: lane lc takes row lc & 3, then each row's values
+    // are broadcast across the quad (DPP), instead of every lane loading all
+    // four rows.  A quad's 4 * VEC columns lie in one mask word (VEC divides
+    // 8), the word of the quad's first lane, which idle lanes take too.
+    constexpr bool kQuadEpi = LGW_T >= 4;
+    const int q_row = lc & 3;
+    const uint32_t m_word_q =
+        static_cast<uint32_t>(min(((lc & ~3) * VEC) >> 5, MW - 1)) * 4;
     const uint2 *t_desc = s_sdesc;
     const uint32_t *t_piece = s_piece;
     int64_t sub = 0;
@@ -559,17 +568,30 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
         // (the 24-bit products ignore the feature bits of .y)
 #pragma unroll
         for (int i = 0; i < kL; ++i) load_grad_buf<GD, VEC, kGCpol>(grs, __umul24(dv[i].y, rowFb) + flb, gv[i]);
-        if constexpr (kRelu) {
+        if constexpr (kQuadEpi && (kRelu || kLin)) {
+            // this lane's row of the quad (selects on named values: indexing
+            // the descriptor array would put it in scratch memory)
+            const uint32_t y0 = dv[0].y, y1 = dv[1].y, y2 = dv[2].y, y3 = dv[3].y;
+            const uint32_t yq = (q_row & 2) ? ((q_row & 1) ? y3 : y2) : ((q_row & 1) ? y1 : y0);
+            if constexpr (kRelu)
+                mv[0] = __builtin_amdgcn_raw_buffer_load_b32(
+                    mrs, __umul24(yq, rowMb) + flp * static_cast<uint32_t>(MW) * 4 + m_word_q, 0, 0);
+            if constexpr (kLin)
+                xv[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    xrs, __umul24(yq, static_cast<uint32_t>(F) * 4) + flp * 4, 0, 0));
+        } else {
+            if constexpr (kRelu) {
 #pragma unroll
-            for (int i = 0; i < kL; ++i)
-                mv[i] = __builtin_amdgcn_raw_buffer_load_b32(
-                    mrs, __umul24(dv[i].y, rowMb) + flp * static_cast<uint32_t>(MW) * 4 + m_word_off, 0, 0);
-        }
-        if constexpr (kLin) {
+                for (int i = 0; i < kL; ++i)
+                    mv[i] = __builtin_amdgcn_raw_buffer_load_b32(
+                        mrs, __umul24(dv[i].y, rowMb) + flp * static_cast<uint32_t>(MW) * 4 + m_word_off, 0, 0);
+            }
+            if constexpr (kLin) {
 #pragma unroll
-            for (int i = 0; i < kL; ++i)
-                xv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                    xrs, __umul24(dv[i].y, static_cast<uint32_t>(F) * 4) + flp * 4, 0, 0));
+                for (int i = 0; i < kL; ++i)
+                    xv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                        xrs, __umul24(dv[i].y, static_cast<uint32_t>(F) * 4) + flp * 4, 0, 0));
+            }
         }
     };
 
@@ -614,6 +636,10 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
             const float qf = __uint_as_float(dsc[i].x);
             float gq[VEC], gm[VEC];
             float dot = 0.0f, dot2 = 0.0f, dotl = 0.0f;
+            uint32_t mvi = 0;
+            float xvi = 0.0f;
+            if constexpr (kRelu) mvi = kQuadEpi ? quad_bcast(mv[0], i) : mv[i];
+            if constexpr (kLin) xvi = kQuadEpi ? __uint_as_float(quad_bcast(__float_as_uint(xv[0]), i)) : xv[i];
 #pragma unroll
             for (int q = 0; q < VEC; ++q) {
                 // ReLU: the forward's pass bit of column lc * VEC + q
@@ -621,13 +647,13 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
                 if constexpr (kRelu)
                     gm[q] = __uint_as_float(__float_as_uint(gm[q]) &
                                             static_cast<uint32_t>(__builtin_amdgcn_sbfe(
-                                                static_cast<int>(mv[i]), m_shift + q, 1)));
+                                                static_cast<int>(mvi), m_shift + q, 1)));
                 gq[q] = quant<Q>(gm[q]);
                 ab[q] += gq[q];
                 aw[q] = fmaf(qf, gq[q], aw[q]);
                 if constexpr (kRawDb) ad[q] += kLin ? gv[i][q] : gm[q];
                 if constexpr (kLin) {
-                    ax[q] = fmaf(gv[i][q], xv[i], ax[q]);
+                    ax[q] = fmaf(gv[i][q], xvi, ax[q]);
                     dotl = fmaf(gv[i][q], lw[q], dotl);
                 }
                 dot = fmaf(gq[q], wk[q], dot);
@@ -1343,6 +1369,7 @@ template <int GD, int Q, int EPI, int RB>
 hipError_t launch_reduce_epi(const BwdArgs &a, int vec, dim3 grid, size_t lds, hipStream_t s) {
     if (vec == 4) {
         switch (a.LGW) {
+            case 2: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 2, EPI, RB>), grid, dim3(RB), lds, s, a); break;
             case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 4, EPI, RB>), grid, dim3(RB), lds, s, a); break;
             case 8: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 8, EPI, RB>), grid, dim3(RB), lds, s, a); break;
             default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 16, EPI, RB>), grid, dim3(RB), lds, s, a); break;

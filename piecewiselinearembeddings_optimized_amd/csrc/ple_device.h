@@ -243,6 +243,18 @@ __device__ __forceinline__ float dpp_f32(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+// Lane i of each quad of lanes, to all four (quad_perm [i,i,i,i]); i must fold
+// to a constant (an unrolled loop index).  All lanes of the quad must be active.
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v, int i) {
+    const int s = static_cast<int>(v);
+    switch (i) {
+        case 0: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, s, 0x00, 0xF, 0xF, false));
+        case 1: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, s, 0x55, 0xF, 0xF, false));
+        case 2: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, s, 0xAA, 0xF, 0xF, false));
+        default: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, s, 0xFF, 0xF, 0xF, false));
+    }
+}
+
 // Sum over aligned groups of W lanes (W a power of two); every lane of the
 // group receives the sum.  Groups of up to 16 lanes reduce with DPP inside a
 // 16-lane row (quad permutes, then half-row and row mirrors); wider groups

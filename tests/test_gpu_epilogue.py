@@ -134,6 +134,45 @@ def test_backward_epilogue_matches_oracle(cfg, quant, version, relu):
     _check_backward(w, w0, b0, g, version, relu, quant, mask, grads)
 
 
+def _setup_shape(n, f, bmax, d, seed):
+    """Random edges (ragged bin counts), x with exact edge hits, and the
+    linear0 parameters and gradient of `_setup`, at any shape."""
+    rng = np.random.default_rng(seed)
+    bins = []
+    for j in range(f):
+        nb = bmax if j == 0 else int(rng.integers(1, bmax + 1))
+        bins.append(np.cumsum(rng.uniform(0.05, 1.0, nb + 1)).astype(np.float32) - np.float32(nb * 0.25))
+    edges, iw, nbins = workloads.pad_bins(bins)
+    x = (rng.standard_normal((n, f)) * 3).astype(np.float32)
+    for j, e in enumerate(bins):
+        hit = rng.random(n) < 0.1
+        x[hit, j] = e[rng.integers(0, e.size, int(hit.sum()))]
+    wt = rng.uniform(-0.5, 0.5, (f, bmax, d)).astype(np.float32)
+    b = rng.uniform(-0.2, 0.2, (f, d)).astype(np.float32)
+    w = workloads.Workload(f"rand{n}x{f}x{bmax}x{d}", x, bins, edges, iw, nbins, wt, b)
+    w0 = rng.uniform(-0.3, 0.3, size=(f, d)).astype(np.float32)
+    b0 = rng.uniform(-0.3, 0.3, size=(f, d)).astype(np.float32)
+    g = rng.standard_normal((n, f, d)).astype(np.float32)
+    return w, w0, b0, g
+
+
+# Embedding widths whose lane groups differ from the configs': two-lane groups
+# (d = 8, 4 columns a lane), a group of four with one idle lane (12), and
+# ReLU masks of two words where a quad of lanes holds both active and idle
+# lanes (40, 44).
+@pytest.mark.parametrize("d", [8, 12, 40, 44])
+@pytest.mark.parametrize("version,relu", [("A", True), ("B", True), ("B", False)])
+def test_backward_epilogue_lane_group_widths(d, version, relu):
+    w, w0, b0, g = _setup_shape(1500, 7, 40, d, seed=d)
+    print(f"backward_epilogue {w.name} version={version} relu={relu}", flush=True)
+    (x, e, iw, nb, wt, lw), _, idx, mask = _run_forward(w, w0, b0, version, relu, "f32")
+    a = version == "A"
+    grads = ops.backward_epilogue(_t(g), x, e, iw, nb, wt, idx, mask, lw, relu, torch.float32,
+                                  True, True, a, not a, not a)
+    torch.cuda.synchronize()
+    _check_backward(w, w0, b0, g, version, relu, "f32", mask, grads)
+
+
 @pytest.mark.parametrize("version,relu", [("A", True), ("B", True), ("B", False)])
 def test_fallback_backward_epilogue_matches_oracle(version, relu, monkeypatch):
     """The shapes that leave the sorted path (PLE_BWD_SIMPLE=1 forces it)."""
