@@ -486,10 +486,11 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
     const uint32_t Db = static_cast<uint32_t>(D) * esz;
     // Gradient rows spanning 128 bytes or more are streamed (non-temporal
     // loads); narrower rows share lines with a neighbouring feature's rows,
-    // which another run or workgroup reads later.  (Fixed per instantiation:
+    // which another run or workgroup reads later, and so do the rows of
+    // 2-float lanes (D = 2 mod 4).  (Fixed per instantiation:
     // a branch between the two forms around the loads costs more than it
     // saves.)
-    constexpr int kGCpol = LGW_T * VEC * static_cast<int>(esz) >= 128 ? kCpolNT : 0;
+    constexpr int kGCpol = VEC % 4 == 0 && LGW_T * VEC * static_cast<int>(esz) >= 128 ? kCpolNT : 0;
     // idle lanes: an offset past every span
     const uint32_t laneoff = c_ok ? static_cast<uint32_t>(lc) * VEC * esz : 0x80000000u;
     // epilogue inputs of a row (sample s, local feature fl): its mask word
@@ -1223,6 +1224,9 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
         // two waves per SIMD only, which hides less latency; lane groups of a
         // power-of-two width
         int vec = !g_align16 ? 1 : (D % 4 == 0 ? 4 : 1);
+        // even D not a multiple of 4 (up to 32 columns): 2 floats per lane,
+        // half the loads of one per lane and lane groups with DPP sums
+        if (vec == 1 && g_align16 && D % 2 == 0 && D >= 6 && D <= 32) vec = 2;
         const int vec_env = env_int("PLE_BWD_VEC", 0);    // tuning: 8 or 1 instead of the default
         if (vec_env == 8 && D % 8 == 0 && g_align16 && !lin) vec = 8;
         if (vec_env == 1) vec = 1;
@@ -1363,8 +1367,9 @@ hipError_t launch_sort(const BwdArgs &a, int idxb, dim3 grid, size_t lds, hipStr
     return hipGetLastError();
 }
 
-// Lane-group width as a template argument for the 8- and 4-float rows (DPP
-// reductions); the one-column-per-lane variant takes it at run time.
+// Lane-group width as a template argument (DPP reductions) for the 4- and
+// 2-float rows and the common one-column-a-lane widths; the other widths of
+// one column a lane take it at run time.
 template <int GD, int Q, int EPI, int RB>
 hipError_t launch_reduce_epi(const BwdArgs &a, int vec, dim3 grid, size_t lds, hipStream_t s) {
     if (vec == 4) {
@@ -1374,8 +1379,22 @@ hipError_t launch_reduce_epi(const BwdArgs &a, int vec, dim3 grid, size_t lds, h
             case 8: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 8, EPI, RB>), grid, dim3(RB), lds, s, a); break;
             default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 16, EPI, RB>), grid, dim3(RB), lds, s, a); break;
         }
+    } else if (vec == 2) {
+        // (the planner takes 2 per lane for 6 <= D <= 32: groups of 4 to 16 lanes)
+        switch (a.LGW) {
+            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 2, 4, EPI, RB>), grid, dim3(RB), lds, s, a); break;
+            case 8: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 2, 8, EPI, RB>), grid, dim3(RB), lds, s, a); break;
+            case 16: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 2, 16, EPI, RB>), grid, dim3(RB), lds, s, a); break;
+            default: return hipErrorInvalidConfiguration;
+        }
     } else {
-        hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 0, EPI, RB>), grid, dim3(RB), lds, s, a);
+        // one column a lane: DPP group sums for the 16- and 32-lane groups
+        // (9 <= D <= 32), shuffles at run time for the others
+        switch (a.LGW) {
+            case 16: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 16, EPI, RB>), grid, dim3(RB), lds, s, a); break;
+            case 32: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 32, EPI, RB>), grid, dim3(RB), lds, s, a); break;
+            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 0, EPI, RB>), grid, dim3(RB), lds, s, a); break;
+        }
     }
     return hipGetLastError();
 }

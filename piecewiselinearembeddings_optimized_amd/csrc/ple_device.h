@@ -170,8 +170,8 @@ __device__ __forceinline__ void load_grad_buf(__amdgpu_buffer_rsrc_t rs, uint32_
     }
 }
 
-// VEC consecutive floats from / to LDS (16-byte accesses for VEC 4 and 8;
-// the address is 16-byte aligned in those cases).
+// VEC consecutive floats from / to LDS (16-byte accesses for VEC 4 and 8,
+// 8-byte for VEC 2; the address is aligned to the access in those cases).
 template <int VEC>
 __device__ __forceinline__ void lds_load_vec(const float *p, float *v) {
     if constexpr (VEC % 4 == 0) {
@@ -180,6 +180,9 @@ __device__ __forceinline__ void lds_load_vec(const float *p, float *v) {
             const float4 t = reinterpret_cast<const float4 *>(p)[q];
             v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
         }
+    } else if constexpr (VEC == 2) {
+        const float2 t = *reinterpret_cast<const float2 *>(p);
+        v[0] = t.x; v[1] = t.y;
     } else {
 #pragma unroll
         for (int t = 0; t < VEC; ++t) v[t] = p[t];
@@ -192,14 +195,22 @@ __device__ __forceinline__ void lds_store_vec(float *p, const float *v) {
 #pragma unroll
         for (int q = 0; q < VEC / 4; ++q)
             reinterpret_cast<float4 *>(p)[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    } else if constexpr (VEC == 2) {
+        *reinterpret_cast<float2 *>(p) = make_float2(v[0], v[1]);
     } else {
 #pragma unroll
         for (int t = 0; t < VEC; ++t) p[t] = v[t];
     }
 }
 
-// Stores VEC consecutive outputs as OUT (VEC in {1, 4}; 8 for 16-bit OUT), with the
-// non-temporal hint: the output is written once and not read back here.
+// Stores VEC consecutive outputs as OUT (VEC in {1, 2, 4}; 8 for 16-bit OUT).
+// Four or more outputs a lane, and pairs of 16-bit outputs, are stored with
+// the non-temporal hint (the output is written once and not read back here);
+// one or two fp32 outputs and single 16-bit outputs (rows of D not a multiple
+// of 4, resp. odd D) are plain stores, since with the hint they measured up to
+// 40% slower (F=128, 48 bins, N=65536: d=30 fp32 456 -> 321 us, d=31 484 ->
+// 340 us, d=15 bf16 188 -> 165 us without it; pairs of bf16 at d=30 were
+// about even).
 template <int OUT, int VEC>
 __device__ __forceinline__ void store_out(void *base, int64_t i, const float *v) {
     if constexpr (OUT == PLE_DTYPE_F32) {
@@ -208,8 +219,10 @@ __device__ __forceinline__ void store_out(void *base, int64_t i, const float *v)
             typedef float f32x4 __attribute__((ext_vector_type(4)));
             const f32x4 t = {v[0], v[1], v[2], v[3]};
             __builtin_nontemporal_store(t, reinterpret_cast<f32x4 *>(p));
+        } else if constexpr (VEC == 2) {
+            *reinterpret_cast<float2 *>(p) = make_float2(v[0], v[1]);
         } else {
-            __builtin_nontemporal_store(v[0], p);
+            p[0] = v[0];
         }
     } else {
         uint16_t h[VEC];
@@ -228,8 +241,11 @@ __device__ __forceinline__ void store_out(void *base, int64_t i, const float *v)
             const u32x2 w = {static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16),
                              static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16)};
             __builtin_nontemporal_store(w, reinterpret_cast<u32x2 *>(p));
+        } else if constexpr (VEC == 2) {
+            __builtin_nontemporal_store(static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16),
+                                        reinterpret_cast<uint32_t *>(p));
         } else {
-            __builtin_nontemporal_store(h[0], p);
+            p[0] = h[0];
         }
     }
 }

@@ -129,7 +129,8 @@ __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
                         dst[h + 3] = quant<Q>(w.w);
                     }
                 } else {
-                    dst[0] = quant<Q>(src[0]);
+#pragma unroll
+                    for (int h = 0; h < VEC; ++h) dst[h] = quant<Q>(src[h]);
                 }
             }
         }
@@ -259,6 +260,12 @@ __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
                         r[h + 2] = fmaf(qs[q], W.z, P.z);
                         r[h + 3] = fmaf(qs[q], W.w, P.w);
                     }
+                } else if constexpr (VEC == 2) {
+                    // (8-byte LDS reads: D, the row stride and o_u * VEC are even)
+                    const float2 P = *reinterpret_cast<const float2 *>(row);
+                    const float2 W = *reinterpret_cast<const float2 *>(row + D);
+                    r[0] = fmaf(qs[q], W.x, P.x);
+                    r[1] = fmaf(qs[q], W.y, P.y);
                 } else {
                     r[0] = fmaf(qs[q], row[D], row[0]);
                 }
@@ -329,7 +336,9 @@ constexpr int kOutPerTable = 10;
 bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, bool aligned16, bool out16, FwdPlan &pl) {
     // 16-bit outputs: 8 per lane (one 16-byte store) when D allows, so a
     // store instruction carries as many bytes as fp32's 4 per lane
-    pl.vec = (D % 4 == 0 && aligned16) ? 4 : 1;
+    // Even D not a multiple of 4: 2 per lane (8-byte stores), half the store
+    // instructions and table reads of one per lane
+    pl.vec = (D % 4 == 0 && aligned16) ? 4 : ((D % 2 == 0 && aligned16 && env_int("PLE_FWD_VEC", 0) != 1) ? 2 : 1);
     if (out_bytes == 2 && D % 8 == 0 && aligned16 && out16 && env_int("PLE_FWD_VEC", 0) != 4) pl.vec = 8;
     const int U = static_cast<int>(D / pl.vec);
     if (U > kWave) return false;
@@ -380,8 +389,9 @@ hipError_t launch_vec(const FwdArgs &a, int vec, int idxb, dim3 grid, size_t lds
     if constexpr (OUT != PLE_DTYPE_F32 && EPI == kEpiNone) {
         if (vec == 8) return launch_idx<Q, OUT, EPI, 8>(a, idxb, grid, lds, s);
     }
-    return vec == 4 ? launch_idx<Q, OUT, EPI, 4>(a, idxb, grid, lds, s)
-                    : launch_idx<Q, OUT, EPI, 1>(a, idxb, grid, lds, s);
+    if (vec == 4) return launch_idx<Q, OUT, EPI, 4>(a, idxb, grid, lds, s);
+    if (vec == 2) return launch_idx<Q, OUT, EPI, 2>(a, idxb, grid, lds, s);
+    return launch_idx<Q, OUT, EPI, 1>(a, idxb, grid, lds, s);
 }
 
 // Supported (quant, output) pairs: output == quant without an epilogue (the

@@ -157,10 +157,11 @@ def _setup_shape(n, f, bmax, d, seed):
 
 
 # Embedding widths whose lane groups differ from the configs': two-lane groups
-# (d = 8, 4 columns a lane), a group of four with one idle lane (12), and
-# ReLU masks of two words where a quad of lanes holds both active and idle
-# lanes (40, 44).
-@pytest.mark.parametrize("d", [8, 12, 40, 44])
+# (d = 8, 4 columns a lane), a group of four with one idle lane (12), one
+# column a lane in 16- and 32-lane groups (15, 23), two columns a lane (30),
+# and ReLU masks of two words where a quad of lanes holds both active and
+# idle lanes (40, 44).
+@pytest.mark.parametrize("d", [8, 12, 15, 23, 30, 40, 44])
 @pytest.mark.parametrize("version,relu", [("A", True), ("B", True), ("B", False)])
 def test_backward_epilogue_lane_group_widths(d, version, relu):
     w, w0, b0, g = _setup_shape(1500, 7, 40, d, seed=d)

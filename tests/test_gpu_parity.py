@@ -266,6 +266,10 @@ SHAPES = [
     (2500, 17, 64, 64), (513, 6, 256, 24), (64, 33, 2, 3), (1025, 4, 130, 2), (700, 2, 1000, 8),
     # finalize without an LDS table (B * 2 * 8 * 4 bytes > 160 KiB) over several chunks summed first
     (3000, 2, 3000, 4),
+    # even widths that are not multiples of 4: two columns a lane (lane groups of 4, 8 and 16)
+    (500, 4, 9, 6), (900, 5, 33, 10), (1200, 6, 64, 14), (640, 3, 50, 18), (410, 2, 17, 26), (777, 3, 20, 30),
+    # odd widths: one column a lane in 16- and 32-lane groups
+    (600, 3, 25, 23), (450, 2, 70, 31), (350, 4, 12, 9),
 ]
 
 
@@ -286,6 +290,43 @@ def test_shape_sweep_forward_and_backward(shape, c_oracle):
     gx2, _, _ = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, True, False, False)
     _, gw2, gb2 = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, False, True, True)
     assert torch.equal(gx, gx2) and torch.equal(gw, gw2) and torch.equal(gb, gb2)
+
+
+@pytest.mark.parametrize("d", [10, 30])
+@pytest.mark.parametrize("quant", ["bf16", "f16"])
+def test_two_column_lanes_16bit(d, quant, c_oracle):
+    """16-bit outputs and gradients at even widths that are not multiples of
+    4 (two columns a lane: 4-byte stores and loads): forward bit-exact against
+    the C mirror, backward against the quantisation-aware float64 oracle."""
+    n, f, bmax = 1500, 5, 40
+    w = _random_case(n, f, bmax, d, seed=d + 7)
+    print(f"two-column lanes {w.name} {quant}", flush=True)
+    x, e, iw, nb, wt, bt = _inputs(w)
+    out, idx = ops.forward(x, e, iw, nb, wt, QUANT_TORCH[quant])
+    np.testing.assert_array_equal(idx.cpu().numpy().astype(np.int64), po.bin_indices(w.x, w.edges, w.n_bins))
+    mirror, _ = c_oracle.forward_f32(w.x, w.edges, w.inv_widths, w.n_bins, w.weight, quant=quant)
+    np.testing.assert_array_equal(out.float().cpu().numpy().view(np.uint32), mirror.view(np.uint32))
+    g_h = torch.from_numpy(_grad((n, f, d), d)).to(QUANT_TORCH[quant])
+    gx, gw = ops.backward(g_h.to(DEV), x, e, iw, nb, wt, idx, True, True)
+    torch.cuda.synchronize()
+    _check_backward(w, quant, g_h.float().numpy(), gx, gw, None, c_oracle)
+
+
+@pytest.mark.parametrize("d", [10, 30])
+def test_two_column_lanes_match_one_column_lanes(d, c_oracle, monkeypatch):
+    """The one-column-a-lane forms (PLE_FWD_VEC=1, PLE_BWD_VEC=1) at the same
+    even widths: forward bits equal, backward within the fp32 bar of the oracle."""
+    w = _random_case(1100, 3, 30, d, seed=d + 11)
+    x, e, iw, nb, wt, bt = _inputs(w)
+    g = _grad((1100, 3, d), d + 1)
+    out2, _ = ops.forward_with_bias(x, e, iw, nb, wt, bt, torch.float32)
+    monkeypatch.setenv("PLE_FWD_VEC", "1")
+    monkeypatch.setenv("PLE_BWD_VEC", "1")
+    out1, idx1 = ops.forward_with_bias(x, e, iw, nb, wt, bt, torch.float32)
+    gx, gw, gb = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx1, torch.float32, True, True, True)
+    torch.cuda.synchronize()
+    assert torch.equal(out1.view(torch.int32), out2.view(torch.int32))
+    _check_backward(w, "f32", g, gx, gw, gb, c_oracle)
 
 
 @pytest.mark.parametrize("cfg", [1, 3])
