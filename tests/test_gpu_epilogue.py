@@ -161,17 +161,18 @@ def _setup_shape(n, f, bmax, d, seed):
 # column a lane in 16- and 32-lane groups (15, 23), two columns a lane (30),
 # and ReLU masks of two words where a quad of lanes holds both active and
 # idle lanes (40, 44).
-@pytest.mark.parametrize("d", [8, 12, 15, 23, 30, 40, 44])
+@pytest.mark.parametrize("d,quant", [(8, "f32"), (12, "f32"), (15, "f32"), (23, "f32"), (30, "f32"), (40, "f32"),
+                                     (44, "f32"), (15, "bf16"), (30, "bf16"), (44, "bf16")])
 @pytest.mark.parametrize("version,relu", [("A", True), ("B", True), ("B", False)])
-def test_backward_epilogue_lane_group_widths(d, version, relu):
+def test_backward_epilogue_lane_group_widths(d, quant, version, relu):
     w, w0, b0, g = _setup_shape(1500, 7, 40, d, seed=d)
-    print(f"backward_epilogue {w.name} version={version} relu={relu}", flush=True)
-    (x, e, iw, nb, wt, lw), _, idx, mask = _run_forward(w, w0, b0, version, relu, "f32")
+    print(f"backward_epilogue {w.name} quant={quant} version={version} relu={relu}", flush=True)
+    (x, e, iw, nb, wt, lw), _, idx, mask = _run_forward(w, w0, b0, version, relu, quant)
     a = version == "A"
-    grads = ops.backward_epilogue(_t(g), x, e, iw, nb, wt, idx, mask, lw, relu, torch.float32,
+    grads = ops.backward_epilogue(_t(g), x, e, iw, nb, wt, idx, mask, lw, relu, QT[quant],
                                   True, True, a, not a, not a)
     torch.cuda.synchronize()
-    _check_backward(w, w0, b0, g, version, relu, "f32", mask, grads)
+    _check_backward(w, w0, b0, g, version, relu, quant, mask, grads)
 
 
 @pytest.mark.parametrize("version,relu", [("A", True), ("B", True), ("B", False)])
