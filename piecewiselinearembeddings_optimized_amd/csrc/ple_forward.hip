@@ -48,6 +48,7 @@ struct FwdArgs {
     int G;        // feature groups = ceil(F / FS)
     int C;        // sample chunks
     int64_t NC;   // samples per chunk
+    int FB;       // threads per workgroup (kBlock or 2 * kBlock)
 };
 
 size_t fwd_lds_bytes(int FS, int B, int D) {
@@ -73,8 +74,11 @@ __device__ __forceinline__ uint32_t row_or(uint32_t v, int U, int lane, int u) {
     return acc;
 }
 
-template <int Q, int OUT, int EPI, int VEC, typename IdxT>
-__global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
+// FB: threads per workgroup (256, or 512 where the tables leave room for at
+// most two workgroups per CU: twice the waves per staged table)
+template <int Q, int OUT, int EPI, int VEC, typename IdxT, int FB>
+__global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
+    constexpr int kWaves = FB / kWave;
     constexpr bool HAS_BIAS = EPI == kEpiBias || EPI == kEpiBiasRelu;
     constexpr bool RELU = EPI == kEpiBiasRelu || EPI == kEpiLinRelu;
     constexpr bool LIN = EPI == kEpiLin || EPI == kEpiLinRelu;
@@ -96,19 +100,19 @@ __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
     const int tid = threadIdx.x;
 
     // ---- stage the per-feature tables ------------------------------------
-    for (int i = tid; i < FS; i += kBlock) snb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
-    for (int i = tid; i < FS * (B + 1); i += kBlock) {
+    for (int i = tid; i < FS; i += FB) snb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
+    for (int i = tid; i < FS * (B + 1); i += FB) {
         const int fl = i / (B + 1);
         sedge[i] = fl < nfh ? a.edges[static_cast<int64_t>(f0) * (B + 1) + i] : 0.0f;
     }
-    for (int i = tid; i < FS * B; i += kBlock) {
+    for (int i = tid; i < FS * B; i += FB) {
         const int fl = i / B;
         siw[i] = fl < nfh ? a.iw[static_cast<int64_t>(f0) * B + i] : 0.0f;
     }
     __syncthreads();
 
     const int U = D / VEC;
-    for (int i = tid; i < FS * B * U; i += kBlock) {
+    for (int i = tid; i < FS * B * U; i += FB) {
         const int fl = i / (B * U);
         const int r = i - fl * (B * U);
         const int k = r / U;
@@ -138,7 +142,7 @@ __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
     __syncthreads();
 
     // prefix over logical bins, one lane per (feature, column), in bin order
-    for (int col = tid; col < FS * D; col += kBlock) {
+    for (int col = tid; col < FS * D; col += FB) {
         const int fl = col / D;
         const int j = col - fl * D;
         if (fl < nfh) {
@@ -220,13 +224,13 @@ __global__ __launch_bounds__(kBlock) void ple_fwd_kernel(FwdArgs a) {
     };
     float v_next = load_x(wave);
 
-    for (int64_t t = wave; t < n_tiles; t += kWavesPerBlock) {
+    for (int64_t t = wave; t < n_tiles; t += kWaves) {
         const int64_t n0 = n_begin + t * SW;
         const int64_t pn = n0 + p_s;
         const bool pvalid = p_fok && (pn < n_end);
         const int64_t pidx = pn * F + f0 + p_fl;
         const float v = pvalid ? v_next : 0.0f;
-        v_next = load_x(t + kWavesPerBlock);
+        v_next = load_x(t + kWaves);
         const int k = find_bin(v, e_row, p_n);
         const float frac = (v - e_row[k]) * iw_row[k];
         const float qf = quant<Q>(frac);
@@ -315,7 +319,7 @@ int env_int(const char *name, int dflt) {
 }
 
 struct FwdPlan {
-    int vec, FS, G, C;
+    int vec, FS, G, C, FB;
     int64_t NC;
     size_t lds;
 };
@@ -355,6 +359,16 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
         fs = fs_env;
     pl.lds = fwd_lds_bytes(fs, Bi, Di);
     if (pl.lds > kLdsMax) return false;
+    // 512 threads where the tables leave room for two workgroups per CU or
+    // fewer, and for rows of up to 24 columns: the extra waves hide the bin
+    // search's dependent LDS reads, which weigh more the fewer bytes a pair
+    // writes, and each table is staged for twice as many of them.  Measured
+    // (F=128, 48 bins, N=65536 unless named): c4 204 -> 151 us, c3 157 -> 125
+    // us, d=12 97 -> 86 us, d=24 184 -> 175 us; d=32 (c1) and d=48 the same,
+    // d=64 +7 us.  PLE_FWD_FB overrides it.
+    pl.FB = (kLdsMax / pl.lds < 3 || D <= 24) ? 2 * kBlock : kBlock;
+    const int fb_env = env_int("PLE_FWD_FB", 0);
+    if (fb_env == kBlock || fb_env == 2 * kBlock) pl.FB = fb_env;
     pl.FS = fs;
     pl.G = static_cast<int>((F + fs - 1) / fs);
     const int wg_env = env_int("PLE_FWD_WG_PER_CU", 0);
@@ -378,8 +392,13 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
 template <int Q, int OUT, int EPI, int VEC>
 hipError_t launch_idx(const FwdArgs &a, int idxb, dim3 grid, size_t lds, hipStream_t s) {
     // uint8 indices up to 256 bins, int16 beyond (at most 32766 bins)
-    if (idxb == 1) hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, uint8_t>), grid, dim3(kBlock), lds, s, a);
-    else hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, int16_t>), grid, dim3(kBlock), lds, s, a);
+    if (a.FB == 2 * kBlock) {
+        if (idxb == 1) hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, uint8_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
+        else hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, int16_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
+    } else {
+        if (idxb == 1) hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, uint8_t, kBlock>), grid, dim3(kBlock), lds, s, a);
+        else hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, int16_t, kBlock>), grid, dim3(kBlock), lds, s, a);
+    }
     return hipGetLastError();
 }
 
@@ -430,7 +449,7 @@ int forward_run(const ForwardRequest &r) {
     a.mask = r.relu ? r.mask : nullptr; a.MW = static_cast<int>((r.D + 31) / 32);
     a.out = r.out; a.idx = r.idx;
     a.N = r.N; a.F = static_cast<int>(r.F); a.B = static_cast<int>(r.B); a.D = static_cast<int>(r.D);
-    a.FS = pl.FS; a.G = pl.G; a.C = pl.C; a.NC = pl.NC;
+    a.FS = pl.FS; a.G = pl.G; a.C = pl.C; a.NC = pl.NC; a.FB = pl.FB;
     const int64_t grid = kNumXcd * tiles_per_xcd(pl.G, pl.C);
     if (grid > INT32_MAX) return PLE_E_TOO_LARGE;
     const int idxb = idx_bytes_for(r.B);

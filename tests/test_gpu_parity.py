@@ -122,6 +122,23 @@ def test_forward_16bit_store_widths_agree(cfg, dtype, monkeypatch):
     assert torch.equal(out8.view(torch.int16), out4.view(torch.int16))
 
 
+@pytest.mark.parametrize("cfg", [0, 1, 3, 4])
+def test_forward_workgroup_sizes_agree(cfg, monkeypatch):
+    """256- and 512-thread forward workgroups (PLE_FWD_FB; the planner picks
+    512 for large tables and narrow rows) give the same bits."""
+    w = workloads.make(cfg, REDUCED[cfg])
+    print(f"forward workgroup sizes {w.name}", flush=True)
+    x, e, iw, nb, wt, bt = _inputs(w)
+    dtype = torch.bfloat16 if w.quant == "bf16" else torch.float32
+    outs = []
+    for fb in ("256", "512"):
+        monkeypatch.setenv("PLE_FWD_FB", fb)
+        outs.append(ops.forward(x, e, iw, nb, wt, dtype))
+    monkeypatch.delenv("PLE_FWD_FB")
+    assert torch.equal(outs[0][1], outs[1][1])
+    assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
+
+
 @pytest.mark.parametrize("cfg", [0, 1, 2])
 def test_backward_float16_grad_matches_oracle(cfg, c_oracle):
     """fp16 gradient with fp16 quantisation (the backward of the autocast-fp16
