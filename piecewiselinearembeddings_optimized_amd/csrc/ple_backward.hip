@@ -667,16 +667,20 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
         }
         // dx into LDS by sorted row (rows past the piece's end: the
         // discard slot)
-        if constexpr (LGW_T >= 4 && LGW_T <= 16) {
-            // reduce-scatter: each lane ends with one row's sum
+        if constexpr (LGW_T >= 4 && LGW_T <= 32) {
+            // reduce-scatter: each lane ends with one row's sum (32-lane
+            // groups: within each 16-lane half, then across the halves)
             static_assert(kL == 4, "four rows per piece");
-            constexpr int kLog = LGW_T == 4 ? 2 : (LGW_T == 8 ? 3 : 4);
+            constexpr int kW = LGW_T == 32 ? 16 : LGW_T;
+            constexpr int kLog = kW == 4 ? 2 : (kW == 8 ? 3 : 4);
             const int r = (((lc >> (kLog - 1)) & 1) << 1) | ((lc >> (kLog - 2)) & 1);
             // (selects on named values: indexing the descriptor array
             // with r would put it in scratch memory)
             const uint32_t y0 = dsc[0].y, y1 = dsc[1].y, y2 = dsc[2].y, y3 = dsc[3].y;
             const uint32_t yr = (r & 2) ? ((r & 1) ? y3 : y2) : ((r & 1) ? y1 : y0);
-            s_dx[r < n ? dx_slot(yr) : kP] = group_reduce_scatter4<LGW_T>(parts, lc);
+            float v = group_reduce_scatter4<kW>(parts, lc & (kW - 1));
+            if constexpr (LGW_T == 32) v += __shfl_xor(v, 16);
+            s_dx[r < n ? dx_slot(yr) : kP] = v;
         } else {
 #pragma unroll
             for (int i = 0; i < kL; ++i) {
