@@ -667,11 +667,11 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
         }
         // dx into LDS by sorted row (rows past the piece's end: the
         // discard slot)
-        if constexpr (LGW_T >= 4 && LGW_T <= 32) {
-            // reduce-scatter: each lane ends with one row's sum (32-lane
-            // groups: within each 16-lane half, then across the halves)
+        if constexpr (LGW_T >= 4) {
+            // reduce-scatter: each lane ends with one row's sum (32- and
+            // 64-lane groups: within each 16-lane row, then across the rows)
             static_assert(kL == 4, "four rows per piece");
-            constexpr int kW = LGW_T == 32 ? 16 : LGW_T;
+            constexpr int kW = LGW_T >= 32 ? 16 : LGW_T;
             constexpr int kLog = kW == 4 ? 2 : (kW == 8 ? 3 : 4);
             const int r = (((lc >> (kLog - 1)) & 1) << 1) | ((lc >> (kLog - 2)) & 1);
             // (selects on named values: indexing the descriptor array
@@ -679,7 +679,8 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
             const uint32_t y0 = dsc[0].y, y1 = dsc[1].y, y2 = dsc[2].y, y3 = dsc[3].y;
             const uint32_t yr = (r & 2) ? ((r & 1) ? y3 : y2) : ((r & 1) ? y1 : y0);
             float v = group_reduce_scatter4<kW>(parts, lc & (kW - 1));
-            if constexpr (LGW_T == 32) v += __shfl_xor(v, 16);
+            if constexpr (LGW_T >= 32) v += __shfl_xor(v, 16);
+            if constexpr (LGW_T == 64) v += __shfl_xor(v, 32);
             s_dx[r < n ? dx_slot(yr) : kP] = v;
         } else {
 #pragma unroll
@@ -1228,9 +1229,9 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
         // two waves per SIMD only, which hides less latency; lane groups of a
         // power-of-two width
         int vec = !g_align16 ? 1 : (D % 4 == 0 ? 4 : 1);
-        // even D not a multiple of 4 (up to 32 columns): 2 floats per lane,
+        // even D not a multiple of 4 (up to 64 columns): 2 floats per lane,
         // half the loads of one per lane and lane groups with DPP sums
-        if (vec == 1 && g_align16 && D % 2 == 0 && D >= 6 && D <= 32) vec = 2;
+        if (vec == 1 && g_align16 && D % 2 == 0 && D >= 6 && D <= 64) vec = 2;
         const int vec_env = env_int("PLE_BWD_VEC", 0);    // tuning: 8 or 1 instead of the default
         if (vec_env == 8 && D % 8 == 0 && g_align16 && !lin) vec = 8;
         if (vec_env == 1) vec = 1;
@@ -1384,19 +1385,21 @@ hipError_t launch_reduce_epi(const BwdArgs &a, int vec, dim3 grid, size_t lds, h
             default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 16, EPI, RB>), grid, dim3(RB), lds, s, a); break;
         }
     } else if (vec == 2) {
-        // (the planner takes 2 per lane for 6 <= D <= 32: groups of 4 to 16 lanes)
+        // (the planner takes 2 per lane for 6 <= D <= 64: groups of 4 to 32 lanes)
         switch (a.LGW) {
             case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 2, 4, EPI, RB>), grid, dim3(RB), lds, s, a); break;
             case 8: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 2, 8, EPI, RB>), grid, dim3(RB), lds, s, a); break;
             case 16: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 2, 16, EPI, RB>), grid, dim3(RB), lds, s, a); break;
+            case 32: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 2, 32, EPI, RB>), grid, dim3(RB), lds, s, a); break;
             default: return hipErrorInvalidConfiguration;
         }
     } else {
-        // one column a lane: DPP group sums for the 16- and 32-lane groups
-        // (9 <= D <= 32), shuffles at run time for the others
+        // one column a lane: DPP group sums for the 16- to 64-lane groups
+        // (9 <= D <= 64), shuffles at run time for the others
         switch (a.LGW) {
             case 16: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 16, EPI, RB>), grid, dim3(RB), lds, s, a); break;
             case 32: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 32, EPI, RB>), grid, dim3(RB), lds, s, a); break;
+            case 64: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 64, EPI, RB>), grid, dim3(RB), lds, s, a); break;
             default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 0, EPI, RB>), grid, dim3(RB), lds, s, a); break;
         }
     }

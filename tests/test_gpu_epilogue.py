@@ -158,11 +158,12 @@ def _setup_shape(n, f, bmax, d, seed):
 
 # Embedding widths whose lane groups differ from the configs': two-lane groups
 # (d = 8, 4 columns a lane), a group of four with one idle lane (12), one
-# column a lane in 16- and 32-lane groups (15, 23), two columns a lane (30),
-# and ReLU masks of two words where a quad of lanes holds both active and
-# idle lanes (40, 44).
+# column a lane in 16-, 32- and 64-lane groups (15, 23, 47), two columns a
+# lane (30, 38), and ReLU masks of two words where a quad of lanes holds both
+# active and idle lanes (40, 44).
 @pytest.mark.parametrize("d,quant", [(8, "f32"), (12, "f32"), (15, "f32"), (23, "f32"), (30, "f32"), (40, "f32"),
-                                     (44, "f32"), (15, "bf16"), (30, "bf16"), (44, "bf16")])
+                                     (44, "f32"), (38, "f32"), (47, "f32"), (15, "bf16"), (30, "bf16"),
+                                     (44, "bf16")])
 @pytest.mark.parametrize("version,relu", [("A", True), ("B", True), ("B", False)])
 def test_backward_epilogue_lane_group_widths(d, quant, version, relu):
     w, w0, b0, g = _setup_shape(1500, 7, 40, d, seed=d)

@@ -287,6 +287,8 @@ SHAPES = [
     (500, 4, 9, 6), (900, 5, 33, 10), (1200, 6, 64, 14), (640, 3, 50, 18), (410, 2, 17, 26), (777, 3, 20, 30),
     # odd widths: one column a lane in 16- and 32-lane groups
     (600, 3, 25, 23), (450, 2, 70, 31), (350, 4, 12, 9),
+    # wider ones: two columns a lane in 32-lane groups, one column a lane in 64-lane groups
+    (700, 3, 30, 38), (400, 3, 15, 62), (500, 2, 20, 47),
 ]
 
 
