@@ -359,11 +359,11 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
         while (fs < 8 && fits_wave(fs * 2) && fwd_lds_bytes(fs * 2, Bi, Di) <= 2 * kLdsBudget &&
                F >= 16 * 2 * fs)
             fs *= 2;
-    // One or two columns a lane with a single feature a group (wide D not a
-    // multiple of 4): two features within twice the budget store two rows'
-    // segments a wave instruction (d = 50: 650 -> 450 us, d = 62: 741 -> 544
-    // us at F=128, 48 bins, N=65536)
-    if (pl.vec <= 2 && fs == 1 && fits_wave(2) && fwd_lds_bytes(2, Bi, Di) <= 2 * kLdsBudget) fs = 2;
+    // A single feature a group (wide D): two features within twice the
+    // budget (at F=128, 48 bins, N=65536: d = 44 856 -> 502 us, d = 48 372 ->
+    // 298 us, d = 50 650 -> 450 us, d = 56 793 -> 372 us, d = 62 741 -> 544
+    // us, d = 64 390 -> 340 us)
+    if (fs == 1 && fits_wave(2) && fwd_lds_bytes(2, Bi, Di) <= 2 * kLdsBudget) fs = 2;
     while (static_cast<int64_t>(fs) * D * out_bytes < 128 && fits_wave(fs * 2) &&
            fwd_lds_bytes(fs * 2, Bi, Di) <= kLdsMax)
         fs *= 2;
