@@ -85,7 +85,11 @@ int ple_bin_index_bytes(int64_t max_n_bins);
  * Supported pairings: output_dtype == quant_dtype with bias NULL (the
  * reference operator), or output_dtype == PLE_DTYPE_F32 with a bias (the
  * module's "x_ple + bias" fused into the store); others -> PLE_E_UNSUPPORTED.
- * N may be 0 (no launch).  F, B, D >= 1; D <= 64; B <= 32766.
+ * N may be 0 (no launch).  F, B, D >= 1; D <= 64 (the reference module's
+ * limit); B <= 2^24 and F * B * D < 2^30 (else PLE_E_TOO_LARGE).  Every such
+ * shape runs: per-feature tables that fit LDS take the table kernel, larger
+ * ones (many bins times a wide row) a kernel that keeps prefix checkpoints in
+ * LDS and reads the weights from global memory -- bit-identical results.
  */
 int ple_forward_launch(const float *x, const float *bin_edges, const float *inv_bin_widths,
                        const int32_t *n_bins, const float *weight, const float *bias,
@@ -114,6 +118,8 @@ size_t ple_backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D);
  *   bin_indices     as produced by ple_forward_launch
  *   workspace       >= ple_backward_workspace_bytes(N, F, B, D) bytes,
  *                   256-byte aligned, contents need not be initialised
+ * Shapes as for ple_forward_launch; all of them run (tables beyond the
+ * sorted path's LDS take deterministic fallback kernels).
  */
 int ple_backward_launch(const void *grad_output, const float *x, const float *bin_edges,
                         const float *inv_bin_widths, const int32_t *n_bins,
@@ -192,6 +198,44 @@ int ple_encode_backward_launch(const float *grad_output, const float *x, const f
                                const float *inv_bin_widths, const int32_t *n_bins,
                                const int32_t *offsets, float *grad_x, int64_t N, int64_t F,
                                int64_t B, int64_t total_bins, void *stream);
+
+/*
+ * Planner overrides, for tuning sweeps and for tests that run every kernel
+ * form on the same inputs.  No counterpart in the reference (its launchers
+ * have no knobs).  Each knob holds 0 -- the planner's own choice, the default
+ * -- or a forced value, read by every later launch of the process:
+ *   PLE_TUNE_FWD_FS         features per forward workgroup (power of two)
+ *   PLE_TUNE_FWD_WG_PER_CU  forward workgroups per CU the chunking aims for
+ *   PLE_TUNE_FWD_FB         forward workgroup size (256 or 512 threads)
+ *   PLE_TUNE_FWD_VEC        outputs per lane (1, 2 or 4; 16-bit outputs 8)
+ *   PLE_TUNE_FWD_WIDE       1: the wide-table forward kernel for any shape
+ *   PLE_TUNE_BWD_SIMPLE     1: the fallback backward kernels for any shape
+ *   PLE_TUNE_BWD_SIMPLE_GLOBAL 1: their histogram cells in global memory
+ *   PLE_TUNE_BWD_VEC        gradient floats per lane (1 or 8)
+ *   PLE_TUNE_BWD_FS         features per backward sub-tile (1, 2, 4, 8, 16)
+ *   PLE_TUNE_BWD_RB         reduce workgroup size (256 or 512 threads)
+ *   PLE_TUNE_BWD_DBUF       sub-tile descriptor buffers in LDS (1 or 2)
+ *   PLE_TUNE_BWD_WG_PER_CU  reduce workgroups per CU
+ * A forced value the shape cannot take is ignored.  Returns the knob's
+ * previous value, or PLE_E_BAD_SHAPE for an unknown knob.  Not synchronised
+ * with launches running on other threads.
+ */
+enum {
+    PLE_TUNE_FWD_FS = 0,
+    PLE_TUNE_FWD_WG_PER_CU = 1,
+    PLE_TUNE_FWD_FB = 2,
+    PLE_TUNE_FWD_VEC = 3,
+    PLE_TUNE_FWD_WIDE = 4,
+    PLE_TUNE_BWD_SIMPLE = 5,
+    PLE_TUNE_BWD_SIMPLE_GLOBAL = 6,
+    PLE_TUNE_BWD_VEC = 7,
+    PLE_TUNE_BWD_FS = 8,
+    PLE_TUNE_BWD_RB = 9,
+    PLE_TUNE_BWD_DBUF = 10,
+    PLE_TUNE_BWD_WG_PER_CU = 11,
+    PLE_TUNE_COUNT = 12,
+};
+int ple_set_tuning(int knob, int value);
 
 /* Human-readable name of a return code (static storage). */
 const char *ple_error_string(int code);

@@ -94,10 +94,12 @@ torch.library.register_autograd(
 
 
 def _setup_forward_epilogue_context(ctx: Any, inputs, output) -> None:
-    x, bin_edges, inv_bin_widths, n_bins, weight, _bias, lin_weight, _lin_bias, relu, _save, quant_dtype = inputs
+    x, bin_edges, inv_bin_widths, n_bins, weight, _bias, lin_weight, _lin_bias, relu, save_mask, quant_dtype = inputs
     _out, bin_indices, relu_mask = output
     ctx.save_for_backward(x, bin_edges, inv_bin_widths, n_bins, weight, bin_indices, relu_mask, lin_weight)
     ctx.relu = bool(relu)
+    # (from the flag, not the mask's size: an empty batch saves an empty mask)
+    ctx.saved_mask = bool(save_mask)
     ctx.quant_dtype = quant_dtype
     ctx.mark_non_differentiable(bin_indices, relu_mask)
     ctx.set_materialize_grads(False)
@@ -108,7 +110,7 @@ def _forward_epilogue_backward(ctx: Any, grad_output, _grad_bin_indices, _grad_r
         return (None,) * 11
     x, bin_edges, inv_bin_widths, n_bins, weight, bin_indices, relu_mask, lin_weight = ctx.saved_tensors
     need = [bool(ctx.needs_input_grad[i]) for i in (0, 4, 5, 6, 7)]
-    if ctx.relu and relu_mask.numel() == 0:
+    if ctx.relu and not ctx.saved_mask:
         raise RuntimeError("forward_epilogue was called with save_mask=False; its ReLU cannot be differentiated")
     gx, gw, gb, glw, glb = _ops.backward_epilogue(
         grad_output.contiguous(), x, bin_edges, inv_bin_widths, n_bins, weight, bin_indices, relu_mask,

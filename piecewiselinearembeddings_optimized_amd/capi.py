@@ -20,6 +20,12 @@ import torch
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libple_hip.so")
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+
+# planner overrides (PLE_TUNE_* of the header; 0 = the planner's choice)
+TUNE = {
+    "FWD_FS": 0, "FWD_WG_PER_CU": 1, "FWD_FB": 2, "FWD_VEC": 3, "FWD_WIDE": 4, "BWD_SIMPLE": 5,
+    "BWD_SIMPLE_GLOBAL": 6, "BWD_VEC": 7, "BWD_FS": 8, "BWD_RB": 9, "BWD_DBUF": 10, "BWD_WG_PER_CU": 11,
+}
 _DTYPE_CODES = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
 
 _lib = None
@@ -54,6 +60,7 @@ def lib() -> ctypes.CDLL:
         L.ple_abi_version.argtypes, L.ple_abi_version.restype = [], i32
         L.ple_bin_index_bytes.argtypes, L.ple_bin_index_bytes.restype = [i64], i32
         L.ple_error_string.argtypes, L.ple_error_string.restype = [i32], ctypes.c_char_p
+        L.ple_set_tuning.argtypes, L.ple_set_tuning.restype = [i32, i32], i32
         L.ple_forward_launch.argtypes = [p, p, p, p, p, p, p, p, i64, i64, i64, i64, i32, i32, p]
         L.ple_forward_launch.restype = i32
         L.ple_backward_workspace_bytes.argtypes = [i64, i64, i64, i64]
@@ -72,6 +79,12 @@ def lib() -> ctypes.CDLL:
         L.ple_encode_backward_launch.restype = i32
         _lib = L
     return _lib
+
+
+def set_tuning(knob: str, value: int) -> int:
+    """Sets planner override ``knob`` (a key of :data:`TUNE`); returns the
+    previous value.  0 restores the planner's own choice."""
+    return lib().ple_set_tuning(TUNE[knob], int(value))
 
 
 def check(code: int) -> None:

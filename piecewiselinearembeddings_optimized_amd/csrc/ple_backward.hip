@@ -47,10 +47,10 @@
 // No floating-point atomics anywhere, a fixed order for every sum, so results
 // repeat bitwise.
 //
-// Fallback (shapes whose tables do not fit LDS): ple_bwd_simple_dx_kernel and
-// ple_bwd_simple_hist_kernel, same partial layout, same finalize.
-
-#include <stdlib.h>
+// Fallback (shapes whose tables do not fit the sorted path's LDS, any number
+// of bins): ple_bwd_simple_dx_kernel and ple_bwd_simple_hist_kernel (cells in
+// LDS, or in the partials in global memory when B * D * 8 bytes exceed LDS),
+// same partial layout, same finalize.
 
 #include <algorithm>
 
@@ -883,23 +883,31 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_simple_dx_kernel(BwdArgs a) {
 
 // One wave per (feature, sample chunk); lane j owns column j (D <= 64) and
 // walks the chunk in sample order, folding runs of equal bins into its own
-// LDS cells.
-template <int GD, int Q, typename IdxT>
+// cells: in LDS ({bucket} [B][D] then {weighted} [B][D]), copied to the
+// chunk's partials at the end, or -- GLOBAL, tables beyond LDS -- straight in
+// the chunk's partials [B][2D] in global memory, which only this lane reads
+// and writes.  Either way one fixed order per cell.
+template <int GD, int Q, typename IdxT, bool GLOBAL>
 __global__ __launch_bounds__(kWave) void ple_bwd_simple_hist_kernel(BwdArgs a) {
     extern __shared__ float smem[];
     const int B = a.B, D = a.D, F = a.F;
-    float *hb = smem;
-    float *hw = smem + B * D;
     const int f = blockIdx.x % F;
     const int c = blockIdx.x / F;
     const int j = threadIdx.x;
     const bool jok = j < D;
     const int n_real = clamp_nbins(a.nbins[f], B);
-    for (int i = j; i < n_real * D; i += kWave) {
-        hb[i] = 0.0f;
-        hw[i] = 0.0f;
+    float *dst = a.part + (static_cast<int64_t>(c) * F + f) * B * 2 * D;
+    // bucket / weighted cell of bin k for this lane's column
+    float *hb = GLOBAL ? dst + j : smem + j;
+    float *hw = GLOBAL ? dst + D + j : smem + static_cast<int64_t>(B) * D + j;
+    const int cstride = GLOBAL ? 2 * D : D;
+    if (jok) {
+        for (int k = 0; k < n_real; ++k) {
+            hb[static_cast<int64_t>(k) * cstride] = 0.0f;
+            hw[static_cast<int64_t>(k) * cstride] = 0.0f;
+        }
     }
-    __syncthreads();
+    if constexpr (!GLOBAL) __syncthreads();
     const int64_t n_begin = static_cast<int64_t>(c) * a.NC;
     const int64_t n_end = min(a.N, n_begin + a.NC);
     const float *e = a.edges + static_cast<int64_t>(f) * (B + 1);
@@ -934,8 +942,8 @@ __global__ __launch_bounds__(kWave) void ple_bwd_simple_hist_kernel(BwdArgs a) {
             if (a.lin_w) clw = fmaf(graw, xv[t], clw);
             if (k != kc) {
                 if (kc >= 0 && jok) {
-                    hb[kc * D + j] += cb;
-                    hw[kc * D + j] += cw;
+                    hb[static_cast<int64_t>(kc) * cstride] += cb;
+                    hw[static_cast<int64_t>(kc) * cstride] += cw;
                 }
                 kc = k;
                 cb = gq;
@@ -948,16 +956,17 @@ __global__ __launch_bounds__(kWave) void ple_bwd_simple_hist_kernel(BwdArgs a) {
         }
     }
     if (kc >= 0 && jok) {
-        hb[kc * D + j] += cb;
-        hw[kc * D + j] += cw;
+        hb[static_cast<int64_t>(kc) * cstride] += cb;
+        hw[static_cast<int64_t>(kc) * cstride] += cw;
     }
-    __syncthreads();
-    float *dst = a.part + (static_cast<int64_t>(c) * F + f) * B * 2 * D;
-    for (int i = j; i < n_real * D; i += kWave) {
-        const int k = i / D;
-        const int jj = i - k * D;
-        dst[k * 2 * D + jj] = hb[i];
-        dst[k * 2 * D + D + jj] = hw[i];
+    if constexpr (!GLOBAL) {
+        __syncthreads();
+        for (int i = j; i < n_real * D; i += kWave) {
+            const int k = i / D;
+            const int jj = i - k * D;
+            dst[static_cast<int64_t>(k) * 2 * D + jj] = smem[i];
+            dst[static_cast<int64_t>(k) * 2 * D + D + jj] = smem[static_cast<int64_t>(B) * D + i];
+        }
     }
     if (jok) a.part_db[(static_cast<int64_t>(c) * F + f) * D + j] = cdb;
     if (jok && a.lin_w) a.part_lw[(static_cast<int64_t>(c) * F + f) * D + j] = clw;
@@ -1148,14 +1157,9 @@ constexpr size_t kPartialBudget = 64ull << 20;   // bytes of chunk partials
 // kernel's registers allow two waves per SIMD)
 constexpr size_t kReduceLdsTarget = 80 * 1024;
 
-int env_int(const char *name, int dflt) {
-    const char *s = getenv(name);
-    if (!s || !*s) return dflt;
-    return atoi(s);
-}
-
 struct BwdPlan {
     bool sorted;
+    bool hist_global;   // fallback: histogram cells in global memory (tables beyond LDS)
     int vec;
     int rb;          // reduce workgroup size
     int C, Cd;
@@ -1223,7 +1227,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
     pl.sorted = false;
     // Sorted path: bins fit the 12-bit field of a piece, and a sub-tile's
     // gradient rows span less than 2^31 bytes (32-bit buffer offsets).
-    if (B <= 4096 && static_cast<int64_t>(kP) * F * D * 4 < INT32_MAX && env_int("PLE_BWD_SIMPLE", 0) == 0) {
+    if (B <= 4096 && static_cast<int64_t>(kP) * F * D * 4 < INT32_MAX && tuning(PLE_TUNE_BWD_SIMPLE) == 0) {
         // 4 floats per lane (16-byte loads for fp32 gradients) when D allows:
         // 8 per lane halves the per-row instructions but needs registers for
         // two waves per SIMD only, which hides less latency; lane groups of a
@@ -1232,7 +1236,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
         // even D not a multiple of 4 (up to 64 columns): 2 floats per lane,
         // half the loads of one per lane and lane groups with DPP sums
         if (vec == 1 && g_align16 && D % 2 == 0 && D >= 6 && D <= 64) vec = 2;
-        const int vec_env = env_int("PLE_BWD_VEC", 0);    // tuning: 8 or 1 instead of the default
+        const int vec_env = tuning(PLE_TUNE_BWD_VEC);    // 8 or 1 instead of the default
         if (vec_env == 8 && D % 8 == 0 && g_align16 && !lin) vec = 8;
         if (vec_env == 1) vec = 1;
         const int uv = static_cast<int>(D / vec);
@@ -1255,7 +1259,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                     break;
                 }
             }
-            const int fs_env = env_int("PLE_BWD_FS", 0);
+            const int fs_env = tuning(PLE_TUNE_BWD_FS);
             if (fs_env == 1 || fs_env == 2 || fs_env == 4 || fs_env == 8 || fs_env == 16) {
                 BwdArgs t{};
                 const size_t lds = reduce_layout(t, fs_env, static_cast<int>(B), static_cast<int>(D), LG, pm_for(fs_env), raw_db, lin);
@@ -1275,7 +1279,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                 {
                     const bool wide_ok = !raw_db && vec != 8;
                     bool wide = wide_ok && kLdsMax / best_lds < 2;
-                    const int rb_env = env_int("PLE_BWD_RB", 0);
+                    const int rb_env = tuning(PLE_TUNE_BWD_RB);
                     if (rb_env == kBlock || rb_env == kWideBlock) wide = wide_ok && rb_env == kWideBlock;
                     if (wide) {
                         BwdArgs tw = geo;
@@ -1297,8 +1301,8 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                     BwdArgs t2 = geo;
                     const size_t lds2 = reduce_layout(t2, best_fs, static_cast<int>(B), static_cast<int>(D), LGc, PM,
                                                       raw_db, lin, 2);
-                    const int dbuf_env = env_int("PLE_BWD_DBUF", -1);
-                    const bool dbuf = dbuf_env >= 0 ? (dbuf_env > 0 && lds2 <= kLdsMax) : (kLdsMax / lds2 >= 2);
+                    const int dbuf_k = tuning(PLE_TUNE_BWD_DBUF);   // 1: one buffer, 2: two
+                    const bool dbuf = dbuf_k != 0 ? (dbuf_k == 2 && lds2 <= kLdsMax) : (kLdsMax / lds2 >= 2);
                     if (dbuf) {
                         geo = t2;
                         best_lds = lds2;
@@ -1321,12 +1325,13 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                     int nbits = 0;
                     while ((1ll << nbits) <= B) ++nbits;      // keys 0..B
                     geo.nbits = nbits;
-                    // chunks of sub-tiles: about PLE_BWD_WG_PER_CU reduce
+                    // chunks of sub-tiles: about PLE_TUNE_BWD_WG_PER_CU reduce
                     // workgroups per CU, within the partials budget.  Two per
                     // CU measured best at c1-c3 (4 per CU: +15 to +40 us, the
                     // partials and each workgroup's table staging double)
                     const int64_t per_chunk = F * B * 2 * D * 4;
-                    int64_t c = (static_cast<int64_t>(env_int("PLE_BWD_WG_PER_CU", 2)) * cus + geo.G - 1) / geo.G;
+                    const int wg_k = tuning(PLE_TUNE_BWD_WG_PER_CU);
+                    int64_t c = (static_cast<int64_t>(wg_k > 0 ? wg_k : 2) * cus + geo.G - 1) / geo.G;
                     const int64_t budget_c = static_cast<int64_t>(kPartialBudget) / per_chunk;
                     if (c > budget_c) c = budget_c;
                     if (c > geo.T) c = geo.T;
@@ -1356,7 +1361,10 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
         if (c < 1) c = 1;
         pl.NC = (N + c - 1) / c;
         pl.C = pl.Cd = static_cast<int>((N + pl.NC - 1) / pl.NC);
+        // histogram cells in LDS when they fit, else in the partials themselves
         pl.lds = static_cast<size_t>(B) * D * 2 * sizeof(float);
+        pl.hist_global = pl.lds > kLdsMax || tuning(PLE_TUNE_BWD_SIMPLE_GLOBAL) == 1;
+        if (pl.hist_global) pl.lds = 0;
     }
     pl.part_bytes = static_cast<size_t>(pl.Cd) * F * B * 2 * D * sizeof(float);
     pl.part_db_bytes = static_cast<size_t>(pl.Cd) * F * D * sizeof(float);
@@ -1364,7 +1372,37 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
     return pl;
 }
 
-// Bin indices are uint8 (up to 256 bins) or int16 (up to 32766 bins).
+// Plans depend only on the shape, the gradient's alignment, the epilogue
+// flags, the device's CU count and the tuning knobs: a small per-thread cache
+// keeps the planner off the per-launch path.
+const BwdPlan &plan_cached(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16, bool raw_db, bool lin) {
+    struct Entry {
+        int64_t N, F, B, D;
+        int flags, cus;
+        uint32_t epoch;
+        bool valid;
+        BwdPlan pl;
+    };
+    constexpr int kEntries = 8;
+    thread_local Entry cache[kEntries] = {};
+    thread_local int next = 0;
+    const int cus = device_cu_count();
+    const uint32_t epoch = tuning_epoch();
+    const int flags = (g_align16 ? 1 : 0) | (raw_db ? 2 : 0) | (lin ? 4 : 0);
+    for (const Entry &e : cache)
+        if (e.valid && e.N == N && e.F == F && e.B == B && e.D == D && e.flags == flags && e.cus == cus &&
+            e.epoch == epoch)
+            return e.pl;
+    Entry &e = cache[next];
+    next = (next + 1) % kEntries;
+    e.N = N; e.F = F; e.B = B; e.D = D; e.flags = flags; e.cus = cus; e.epoch = epoch;
+    e.pl = plan_backward(N, F, B, D, g_align16, raw_db, lin);
+    e.valid = true;
+    return e.pl;
+}
+
+// Bin indices are uint8 (up to 256 bins) or int16 (the sorted path takes at
+// most 4096 bins).
 template <int Q>
 hipError_t launch_sort(const BwdArgs &a, int idxb, dim3 grid, size_t lds, hipStream_t s) {
     if (idxb == 1) hipLaunchKernelGGL((ple_bwd_sort_kernel<Q, uint8_t>), grid, dim3(kBlock), lds, s, a);
@@ -1464,14 +1502,21 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
             if (blocks > cap) blocks = cap;
             if (blocks < 1) blocks = 1;
             if (idxb == 1) hipLaunchKernelGGL((ple_bwd_simple_dx_kernel<GD, Q, uint8_t>), dim3(blocks), dim3(kBlock), 0, s, a);
-            else hipLaunchKernelGGL((ple_bwd_simple_dx_kernel<GD, Q, int16_t>), dim3(blocks), dim3(kBlock), 0, s, a);
+            else if (idxb == 2) hipLaunchKernelGGL((ple_bwd_simple_dx_kernel<GD, Q, int16_t>), dim3(blocks), dim3(kBlock), 0, s, a);
+            else hipLaunchKernelGGL((ple_bwd_simple_dx_kernel<GD, Q, int32_t>), dim3(blocks), dim3(kBlock), 0, s, a);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
         if (want_dwdb) {
             const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.F) * pl.C));
-            if (idxb == 1) hipLaunchKernelGGL((ple_bwd_simple_hist_kernel<GD, Q, uint8_t>), grid, dim3(kWave), pl.lds, s, a);
-            else hipLaunchKernelGGL((ple_bwd_simple_hist_kernel<GD, Q, int16_t>), grid, dim3(kWave), pl.lds, s, a);
+            if (pl.hist_global) {
+                if (idxb == 1) hipLaunchKernelGGL((ple_bwd_simple_hist_kernel<GD, Q, uint8_t, true>), grid, dim3(kWave), 0, s, a);
+                else if (idxb == 2) hipLaunchKernelGGL((ple_bwd_simple_hist_kernel<GD, Q, int16_t, true>), grid, dim3(kWave), 0, s, a);
+                else hipLaunchKernelGGL((ple_bwd_simple_hist_kernel<GD, Q, int32_t, true>), grid, dim3(kWave), 0, s, a);
+            } else {
+                if (idxb == 1) hipLaunchKernelGGL((ple_bwd_simple_hist_kernel<GD, Q, uint8_t, false>), grid, dim3(kWave), pl.lds, s, a);
+                else hipLaunchKernelGGL((ple_bwd_simple_hist_kernel<GD, Q, int16_t, false>), grid, dim3(kWave), pl.lds, s, a);
+            }
             e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
@@ -1521,7 +1566,21 @@ hipError_t launch_q(const BwdArgs &a, const BwdPlan &pl, int q, int idxb, bool w
 
 size_t backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D) {
     // the plan depends on the gradient's alignment and dtype; report the largest need
-    // (and on the epilogue: the linear0 sums need their own partials)
+    // (and on the epilogue: the linear0 sums need their own partials).  The
+    // last few answers are kept per thread.
+    struct Entry {
+        int64_t N, F, B, D;
+        int cus;
+        uint32_t epoch;
+        size_t bytes;
+    };
+    constexpr int kEntries = 4;
+    thread_local Entry cache[kEntries] = {};
+    thread_local int next = 0;
+    const int cus = device_cu_count();
+    const uint32_t epoch = tuning_epoch();
+    for (const Entry &e : cache)
+        if (e.cus == cus && e.N == N && e.F == F && e.B == B && e.D == D && e.epoch == epoch) return e.bytes;
     size_t need = 0;
     for (int al = 0; al < 2; ++al)
         for (int raw = 0; raw < 2; ++raw)
@@ -1529,6 +1588,8 @@ size_t backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D) {
                 const size_t t = plan_backward(N, F, B, D, al != 0, raw != 0, lin != 0).total();
                 need = t > need ? t : need;
             }
+    cache[next] = Entry{N, F, B, D, cus, epoch, need};
+    next = (next + 1) % kEntries;
     return need;
 }
 
@@ -1544,8 +1605,7 @@ int backward_run(const BackwardRequest &r) {
     const uintptr_t gaddr = reinterpret_cast<uintptr_t>(r.g);
     const int gbytes = r.grad_dtype == PLE_DTYPE_F32 ? 4 : 2;
     if (gaddr % gbytes != 0) return PLE_E_MISALIGNED;
-    BwdPlan pl = plan_backward(r.N, r.F, r.B, r.D, gaddr % 16 == 0, r.quant != PLE_DTYPE_F32 || lin, lin);
-    if (!pl.sorted && want_dwdb && pl.lds > kLdsMax) return PLE_E_UNSUPPORTED;
+    const BwdPlan &pl = plan_cached(r.N, r.F, r.B, r.D, gaddr % 16 == 0, r.quant != PLE_DTYPE_F32 || lin, lin);
     // the sorted path always needs its descriptors; the fallback only for dW / db
     const size_t need = (pl.sorted || want_dwdb) ? pl.total() : 0;
     if (need > 0 && (r.workspace == nullptr || r.workspace_bytes < need ||

@@ -1,6 +1,8 @@
 // The extern "C" entry points of include/ple_hip.h: argument checks that need
 // no device, then the forward / backward launchers.
 
+#include <atomic>
+
 #include "ple_internal.h"
 
 namespace ple {
@@ -20,9 +22,20 @@ int device_cu_count() {
 
 namespace {
 
+std::atomic<int> g_tuning[PLE_TUNE_COUNT];
+std::atomic<uint32_t> g_tuning_epoch{0};
+
+}  // namespace
+
+int tuning(int knob) { return g_tuning[knob].load(std::memory_order_relaxed); }
+
+uint32_t tuning_epoch() { return g_tuning_epoch.load(std::memory_order_relaxed); }
+
+namespace {
+
 int check_common(int64_t N, int64_t F, int64_t B, int64_t D) {
     if (N < 0 || F < 1 || B < 1 || D < 1) return PLE_E_BAD_SHAPE;
-    if (F > INT32_MAX / 2 || B > 32766 || D > 64) return PLE_E_TOO_LARGE;
+    if (F > INT32_MAX / 2 || B > kMaxBins || D > 64) return PLE_E_TOO_LARGE;
     if (F * (B + 1) > INT32_MAX / 2 || F * B * 2 * D > INT32_MAX) return PLE_E_TOO_LARGE;
     if (N > INT64_MAX / (F * D)) return PLE_E_TOO_LARGE;
     return PLE_OK;
@@ -37,6 +50,13 @@ int ple_abi_version(void) { return (1 << 16) | 1; }
 
 int ple_bin_index_bytes(int64_t max_n_bins) { return ple::idx_bytes_for(max_n_bins); }
 
+int ple_set_tuning(int knob, int value) {
+    if (knob < 0 || knob >= PLE_TUNE_COUNT) return PLE_E_BAD_SHAPE;
+    const int prev = ple::g_tuning[knob].exchange(value, std::memory_order_relaxed);
+    ple::g_tuning_epoch.fetch_add(1, std::memory_order_relaxed);
+    return prev;
+}
+
 const char *ple_error_string(int code) {
     switch (code) {
         case PLE_OK: return "success";
@@ -44,9 +64,9 @@ const char *ple_error_string(int code) {
         case PLE_E_BAD_SHAPE: return "invalid shape (need N >= 0 and F, B, D >= 1)";
         case PLE_E_BAD_DTYPE: return "invalid dtype code";
         case PLE_E_BAD_INDEX_WIDTH: return "invalid bin index width";
-        case PLE_E_TOO_LARGE: return "sizes exceed the supported range (D <= 64, max_n_bins <= 32766)";
+        case PLE_E_TOO_LARGE: return "sizes exceed the supported range (D <= 64, max_n_bins <= 2^24, F * max_n_bins * D < 2^30)";
         case PLE_E_WORKSPACE: return "workspace is NULL, too small or not 256-byte aligned";
-        case PLE_E_UNSUPPORTED: return "combination not supported (dtype pairing, or per-feature tables exceed LDS)";
+        case PLE_E_UNSUPPORTED: return "combination not supported (dtype or epilogue pairing)";
         case PLE_E_MISALIGNED: return "pointer misaligned for its element type";
         default: break;
     }

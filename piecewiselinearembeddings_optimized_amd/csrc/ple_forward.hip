@@ -20,8 +20,13 @@
 //   lin_relu   v = (lin_b + lin_w * x) + relu(x_ple)
 // With ReLU the store also writes one bit per element, set where the ReLU
 // passes its input (input > 0, or NaN), for the backward.
-
-#include <stdlib.h>
+//
+// Tables too large for LDS (many bins times a wide row) take
+// ple_fwd_wide_kernel: LDS holds checkpoints of the prefix every S bins, and
+// each output continues the fold from its checkpoint with weights read from
+// global memory -- the same fp32 additions in the same order, so the same
+// bits (the role of the reference's generic kernel, forward_cuda.cu:293-425,
+// chosen at :478-512).
 
 #include "ple_device.h"
 #include "ple_internal.h"
@@ -49,9 +54,13 @@ struct FwdArgs {
     int C;        // sample chunks
     int64_t NC;   // samples per chunk
     int FB;       // threads per workgroup (kBlock or 2 * kBlock)
+    // wide-table kernel: checkpoint stride (bins), LDS offsets (floats) of
+    // the weight stage and of the edge / inverse-width tables, and whether
+    // the edges and inverse widths are staged in LDS (else read from global)
+    int S, stage_off, edge_off, edges_lds;
 };
 
-size_t fwd_lds_bytes(int FS, int B, int D) {
+size_t fwd_lds_bytes(int64_t FS, int64_t B, int64_t D) {
     return 4 * (static_cast<size_t>(FS) * B * 2 * D   // table {prefix | weight}
                 + static_cast<size_t>(FS) * (B + 1)   // edges
                 + static_cast<size_t>(FS) * B         // inverse widths
@@ -74,13 +83,53 @@ __device__ __forceinline__ uint32_t row_or(uint32_t v, int U, int lane, int u) {
     return acc;
 }
 
+// One lane's VEC results of an output row (fp32 fma of prefix and fraction
+// times weight) rounded through Q, the epilogue applied, stored as OUT at
+// element `oi` of the output.  With ReLU the pass bits of the row's U lanes
+// (this one is lane o_u of them) are gathered into the row's mask words at
+// `mi`.  bvec / lwv: the lane's bias or linear0 weight (linear0 bias in bvec);
+// xs: the sample's x (linear0).
+template <int Q, int OUT, int EPI, int VEC>
+__device__ __forceinline__ void emit_segment(const FwdArgs &a, float (&r)[VEC], const float (&bvec)[VEC],
+                                             const float (&lwv)[VEC], float xs, bool row_ok, int64_t oi,
+                                             int64_t mi, int U, int lane, int o_u, int m_shift, int m_word) {
+    constexpr bool HAS_BIAS = EPI == kEpiBias || EPI == kEpiBiasRelu;
+    constexpr bool RELU = EPI == kEpiBiasRelu || EPI == kEpiLinRelu;
+    constexpr bool LIN = EPI == kEpiLin || EPI == kEpiLinRelu;
+    uint32_t mbits = 0;
+#pragma unroll
+    for (int t2 = 0; t2 < VEC; ++t2) {
+        float o = quant<Q>(r[t2]);
+        if constexpr (HAS_BIAS) o = o + bvec[t2];
+        if constexpr (RELU) {
+            // torch.relu: NaN passes, x <= 0 gives 0
+            const bool pass = !(o <= 0.0f);
+            mbits |= static_cast<uint32_t>(pass) << t2;
+            o = pass ? o : 0.0f;
+        }
+        if constexpr (LIN) o = fmaf(lwv[t2], xs, bvec[t2]) + o;
+        r[t2] = o;
+    }
+    if (row_ok) store_out<OUT, VEC>(a.out, oi, r);
+    if constexpr (RELU) {
+        if (a.mask) {
+            const uint32_t w0 = row_or(m_word == 0 ? mbits << m_shift : 0u, U, lane, o_u);
+            const uint32_t w1 = a.MW > 1 ? row_or(m_word == 1 ? mbits << m_shift : 0u, U, lane, o_u) : 0u;
+            if (row_ok && o_u == 0) {
+                uint32_t *mp = a.mask + mi;
+                mp[0] = w0;
+                if (a.MW > 1) mp[1] = w1;
+            }
+        }
+    }
+}
+
 // FB: threads per workgroup (256, or 512 where the tables leave room for at
 // most two workgroups per CU: twice the waves per staged table)
 template <int Q, int OUT, int EPI, int VEC, typename IdxT, int FB>
 __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
     constexpr int kWaves = FB / kWave;
     constexpr bool HAS_BIAS = EPI == kEpiBias || EPI == kEpiBiasRelu;
-    constexpr bool RELU = EPI == kEpiBiasRelu || EPI == kEpiLinRelu;
     constexpr bool LIN = EPI == kEpiLin || EPI == kEpiLinRelu;
     extern __shared__ float smem[];
     const int FS = a.FS, B = a.B, D = a.D, F = a.F;
@@ -273,35 +322,153 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
                 } else {
                     r[0] = fmaf(qs[q], row[D], row[0]);
                 }
-                uint32_t mbits = 0;
-#pragma unroll
-                for (int t2 = 0; t2 < VEC; ++t2) {
-                    float o = quant<Q>(r[t2]);
-                    if constexpr (HAS_BIAS) o = o + bvec[t2];
-                    if constexpr (RELU) {
-                        // torch.relu: NaN passes, x <= 0 gives 0
-                        const bool pass = !(o <= 0.0f);
-                        mbits |= static_cast<uint32_t>(pass) << t2;
-                        o = pass ? o : 0.0f;
-                    }
-                    if constexpr (LIN) o = fmaf(lwv[t2], xs[q], bvec[t2]) + o;
-                    r[t2] = o;
-                }
                 const bool row_ok = o_ok && s < SW && n < n_end;
-                if (row_ok)
-                    store_out<OUT, VEC>(a.out, n * row_elems + static_cast<int64_t>(f0 + o_fl) * D + o_u * VEC, r);
-                if constexpr (RELU) {
-                    if (a.mask) {
-                        const uint32_t w0 = row_or(m_word == 0 ? mbits << m_shift : 0u, U, lane, o_u);
-                        const uint32_t w1 = a.MW > 1 ? row_or(m_word == 1 ? mbits << m_shift : 0u, U, lane, o_u) : 0u;
-                        if (row_ok && o_u == 0) {
-                            uint32_t *mp = a.mask + (n * F + f0 + o_fl) * a.MW;
-                            mp[0] = w0;
-                            if (a.MW > 1) mp[1] = w1;
-                        }
-                    }
-                }
+                emit_segment<Q, OUT, EPI, VEC>(a, r, bvec, lwv, LIN ? xs[q] : 0.0f, row_ok,
+                                               n * row_elems + static_cast<int64_t>(f0 + o_fl) * D + o_u * VEC,
+                                               (n * F + f0 + o_fl) * a.MW, U, lane, o_u, m_shift, m_word);
             }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// wide tables
+// ---------------------------------------------------------------------------
+
+constexpr int kWideFB = 2 * kBlock;      // threads per wide-table workgroup
+constexpr int kWideStage = 4096;         // weights staged per step of the prefix fold (16 KiB)
+
+// One workgroup per (feature, sample chunk), for per-feature tables that do
+// not fit LDS.  LDS holds the prefix at every S-th bin, cp[m][j] =
+// sum_{i < m S} q(W[f, i, j]), folded in bin order from weights staged through
+// LDS.  An output of bin k starts from cp[k / S] and adds q(W[f, i, j]) for
+// i = S (k / S) .. k - 1 from global memory: the same fp32 additions in the
+// same order as a fold from bin 0, hence the table kernel's bits.  Edges and
+// inverse widths are in LDS when they fit (edges_lds), else the bin search
+// reads them from global memory.  Stores, epilogues and ReLU bits as in the
+// table kernel (one feature a group).
+template <int Q, int OUT, int EPI, int VEC, typename IdxT>
+__global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
+    constexpr int kWaves = kWideFB / kWave;
+    constexpr bool HAS_BIAS = EPI == kEpiBias || EPI == kEpiBiasRelu;
+    constexpr bool LIN = EPI == kEpiLin || EPI == kEpiLinRelu;
+    extern __shared__ float smem[];
+    const int B = a.B, D = a.D, F = a.F, S = a.S;
+    float *cp = smem;                            // [ceil(B / S)][D]
+    float *stage = smem + a.stage_off;           // [kWideStage]
+    float *sedge = smem + a.edge_off;            // [B + 1] (edges_lds)
+    float *siw = sedge + (B + 1);                // [B]     (edges_lds)
+
+    int f, c;
+    if (!decode_tile(blockIdx.x, a.G, a.C, f, c)) return;
+    const int64_t n_begin = static_cast<int64_t>(c) * a.NC;
+    const int64_t n_end = min(a.N, n_begin + a.NC);
+    if (n_begin >= n_end) return;
+    const int tid = threadIdx.x;
+    const int n = clamp_nbins(a.nbins[f], B);
+    const float *wf = a.weight + static_cast<int64_t>(f) * B * D;
+    const float *ef = a.edges + static_cast<int64_t>(f) * (B + 1);
+    const float *iwf = a.iw + static_cast<int64_t>(f) * B;
+    if (a.edges_lds) {
+        // the search reads edges 0..n, the fraction inverse widths 0..n-1
+        for (int i = tid; i <= n; i += kWideFB) sedge[i] = ef[i];
+        for (int i = tid; i < n; i += kWideFB) siw[i] = iwf[i];
+    }
+
+    // ---- prefix checkpoints ------------------------------------------------
+    // Weight rows 0..n-2 enter prefixes (the prefix of bin k sums bins < k,
+    // all identity-mapped below the last bin).  Blocks of kb bins are staged
+    // (contiguous rows of W), then the threads of columns 0..D-1 fold them.
+    const int kb = kWideStage / D;
+    float acc = 0.0f;
+    int next_cp = 0, m_cp = 0;
+    for (int k0 = 0; k0 < n; k0 += kb) {
+        const int nk = min(kb, n - k0);
+        const int nterm = min(nk, n - 1 - k0);       // rows of this block that enter a prefix
+        for (int i = tid; i < nk * D; i += kWideFB)
+            stage[i] = i < nterm * D ? quant<Q>(wf[static_cast<int64_t>(k0) * D + i]) : 0.0f;
+        __syncthreads();
+        if (tid < D) {
+            for (int t = 0; t < nk; ++t) {
+                if (k0 + t == next_cp) {
+                    cp[m_cp * D + tid] = acc;
+                    ++m_cp;
+                    next_cp += S;
+                }
+                acc += stage[t * D + tid];
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- stream wave tiles (one sample a lane, then rows of U lanes) -------
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    const int U = D / VEC;
+    const int R = kWave / U;
+    const float *e_row = a.edges_lds ? sedge : ef;
+    const float *iw_row = a.edges_lds ? siw : iwf;
+    const int o_s = lane / U;
+    const int o_u = lane - o_s * U;
+    const bool o_ok = o_s < R;
+    float bvec[VEC], lwv[VEC];
+#pragma unroll
+    for (int t = 0; t < VEC; ++t) bvec[t] = lwv[t] = 0.0f;
+    if constexpr (HAS_BIAS || LIN) {
+        if (o_ok) {
+            const int64_t pofs = static_cast<int64_t>(f) * D + o_u * VEC;
+#pragma unroll
+            for (int t = 0; t < VEC; ++t) {
+                bvec[t] = HAS_BIAS ? a.bias[pofs + t] : a.lin_b[pofs + t];
+                if constexpr (LIN) lwv[t] = a.lin_w[pofs + t];
+            }
+        }
+    }
+    const int m_shift = (o_u * VEC) & 31;
+    const int m_word = (o_u * VEC) >> 5;
+    const float *wcol = wf + o_u * VEC;            // this lane's columns of W[f]
+    const int64_t rows = n_end - n_begin;
+    const int64_t n_tiles = (rows + kWave - 1) / kWave;
+    const int64_t row_elems = static_cast<int64_t>(F) * D;
+
+    for (int64_t t = wave; t < n_tiles; t += kWaves) {
+        const int64_t n0 = n_begin + t * kWave;
+        const int64_t pn = n0 + lane;
+        const bool pvalid = pn < n_end;
+        const float v = pvalid ? a.x[pn * F + f] : 0.0f;
+        const int k = find_bin(v, e_row, n);
+        const float qf = quant<Q>((v - e_row[k]) * iw_row[k]);
+        if (pvalid) static_cast<IdxT *>(a.idx)[pn * F + f] = static_cast<IdxT>(k);
+
+        for (int sb = 0; sb < kWave; sb += R) {
+            const int s = sb + o_s;
+            const int src = s & (kWave - 1);
+            const int ks = __shfl(k, src);
+            const float qs = __shfl(qf, src);
+            const float xs = LIN ? __shfl(v, src) : 0.0f;
+            const int64_t nn = n0 + s;
+            const bool row_ok = o_ok && s < kWave && nn < n_end;
+            float r[VEC];
+            if (row_ok) {
+                const int m = ks / S;
+                float P[VEC], W[VEC];
+                lds_load_vec<VEC>(cp + m * D + o_u * VEC, P);
+                for (int i = m * S; i < ks; ++i) {
+                    const float *wi = wcol + static_cast<int64_t>(i) * D;
+#pragma unroll
+                    for (int h = 0; h < VEC; ++h) P[h] += quant<Q>(wi[h]);
+                }
+                const float *wk = wcol + static_cast<int64_t>(phys_bin(ks, n, B)) * D;
+#pragma unroll
+                for (int h = 0; h < VEC; ++h) W[h] = quant<Q>(wk[h]);
+#pragma unroll
+                for (int h = 0; h < VEC; ++h) r[h] = fmaf(qs, W[h], P[h]);
+            } else {
+#pragma unroll
+                for (int h = 0; h < VEC; ++h) r[h] = 0.0f;
+            }
+            emit_segment<Q, OUT, EPI, VEC>(a, r, bvec, lwv, xs, row_ok, nn * row_elems + static_cast<int64_t>(f) * D + o_u * VEC,
+                                           (nn * F + f) * a.MW, U, lane, o_u, m_shift, m_word);
         }
     }
 }
@@ -311,18 +478,51 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
 // wide feature groups.  (Measured at F=128, 48 bins, d=32: two features per
 // workgroup, 25 KB, beat one by 3-11 us; four, 50 KB, lost 15-40 us.)
 constexpr size_t kLdsBudget = 32 * 1024;
-
-int env_int(const char *name, int dflt) {
-    const char *s = getenv(name);
-    if (!s || !*s) return dflt;
-    return atoi(s);
-}
+// Each workgroup writes at least this many times the table bytes it stages
+// (see plan_forward).
+constexpr int kOutPerTable = 10;
 
 struct FwdPlan {
     int vec, FS, G, C, FB;
     int64_t NC;
     size_t lds;
+    bool wide = false;                  // ple_fwd_wide_kernel
+    int S = 1, stage_off = 0, edge_off = 0, edges_lds = 0;
 };
+
+// Wide tables: the prefix checkpoints take at most kWideCpBudget bytes of
+// LDS (the smallest stride S that fits), the edges and inverse widths join
+// them when they fit kWideEdgeBudget.
+constexpr size_t kWideCpBudget = 96 * 1024;
+constexpr size_t kWideEdgeBudget = 40 * 1024;
+
+void plan_wide(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, FwdPlan &pl) {
+    pl.wide = true;
+    pl.FS = 1;
+    pl.FB = kWideFB;
+    if (pl.vec == 8) pl.vec = 4;
+    int64_t S = (B * D * 4 + static_cast<int64_t>(kWideCpBudget) - 1) / static_cast<int64_t>(kWideCpBudget);
+    if (S < 1) S = 1;
+    const int64_t ncp = (B + S - 1) / S;
+    pl.S = static_cast<int>(S);
+    pl.stage_off = static_cast<int>(align_up(static_cast<size_t>(ncp * D), 4));
+    pl.edge_off = pl.stage_off + kWideStage;
+    pl.edges_lds = static_cast<size_t>(2 * B + 1) * 4 <= kWideEdgeBudget ? 1 : 0;
+    pl.lds = 4 * (static_cast<size_t>(pl.edge_off) + (pl.edges_lds ? static_cast<size_t>(2 * B + 1) : 0));
+    pl.G = static_cast<int>(F);
+    // chunks: about two workgroups per CU over the grid, each writing at least
+    // kOutPerTable times the weight bytes its prefix pass reads
+    const int64_t target = 2 * static_cast<int64_t>(device_cu_count());
+    int64_t c = (target + F - 1) / F;
+    const int64_t min_nc = (static_cast<int64_t>(kOutPerTable) * B * 4 + out_bytes - 1) / out_bytes;
+    const int64_t c_tbl = (N + min_nc - 1) / min_nc;
+    if (c > c_tbl) c = c_tbl;
+    const int64_t max_c = (N + kWave - 1) / kWave;
+    if (c > max_c) c = max_c;
+    if (c < 1) c = 1;
+    pl.NC = (N + c - 1) / c;
+    pl.C = static_cast<int>((N + pl.NC - 1) / pl.NC);
+}
 
 // FS: the widest power-of-two feature group whose row fits one wave's stores
 // (FS * D/VEC <= 64) and whose tables fit kLdsBudget; then, while a sample's
@@ -333,8 +533,7 @@ struct FwdPlan {
 // at least kOutPerTable times its tables' bytes, since the table staging and
 // the prefix pass are paid per workgroup.  Together, measured: c2 131 -> 59
 // us, c3 186 -> 155 us, c4 517 -> 221 us, c1 unchanged (its plan is the same).
-// PLE_FWD_FS / PLE_FWD_WG_PER_CU override the two choices (tuning).
-constexpr int kOutPerTable = 10;
+// PLE_TUNE_FWD_FS / PLE_TUNE_FWD_WG_PER_CU override the two choices.
 
 // out16: the output's base address is 16-byte aligned (8 outputs per lane)
 bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, bool aligned16, bool out16, FwdPlan &pl) {
@@ -342,10 +541,14 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
     // store instruction carries as many bytes as fp32's 4 per lane
     // Even D not a multiple of 4: 2 per lane (8-byte stores), half the store
     // instructions and table reads of one per lane
-    pl.vec = (D % 4 == 0 && aligned16) ? 4 : ((D % 2 == 0 && aligned16 && env_int("PLE_FWD_VEC", 0) != 1) ? 2 : 1);
-    if (out_bytes == 2 && D % 8 == 0 && aligned16 && out16 && env_int("PLE_FWD_VEC", 0) != 4) pl.vec = 8;
+    pl.vec = (D % 4 == 0 && aligned16) ? 4 : ((D % 2 == 0 && aligned16 && tuning(PLE_TUNE_FWD_VEC) != 1) ? 2 : 1);
+    if (out_bytes == 2 && D % 8 == 0 && aligned16 && out16 && tuning(PLE_TUNE_FWD_VEC) != 4) pl.vec = 8;
     const int U = static_cast<int>(D / pl.vec);
     if (U > kWave) return false;
+    if (fwd_lds_bytes(1, B, D) > kLdsMax || tuning(PLE_TUNE_FWD_WIDE) == 1) {
+        plan_wide(N, F, B, D, out_bytes, pl);
+        return true;
+    }
     const int Bi = static_cast<int>(B), Di = static_cast<int>(D);
     auto fits_wave = [&](int f) { return f <= kWave && f * U <= kWave && (f == 1 || f / 2 < F); };
     int fs = 1;
@@ -367,7 +570,7 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
     while (static_cast<int64_t>(fs) * D * out_bytes < 128 && fits_wave(fs * 2) &&
            fwd_lds_bytes(fs * 2, Bi, Di) <= kLdsMax)
         fs *= 2;
-    const int fs_env = env_int("PLE_FWD_FS", 0);
+    const int fs_env = tuning(PLE_TUNE_FWD_FS);
     if (fs_env > 0 && (fs_env & (fs_env - 1)) == 0 && fs_env * U <= kWave &&
         fwd_lds_bytes(fs_env, Bi, Di) <= kLdsMax)
         fs = fs_env;
@@ -379,13 +582,13 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
     // writes, and each table is staged for twice as many of them.  Measured
     // (F=128, 48 bins, N=65536 unless named): c4 204 -> 151 us, c3 157 -> 125
     // us, d=12 97 -> 86 us, d=24 184 -> 175 us; d=32 (c1) and d=48 the same,
-    // d=64 +7 us.  PLE_FWD_FB overrides it.
+    // d=64 +7 us.  PLE_TUNE_FWD_FB overrides it.
     pl.FB = (kLdsMax / pl.lds < 3 || D <= 24) ? 2 * kBlock : kBlock;
-    const int fb_env = env_int("PLE_FWD_FB", 0);
+    const int fb_env = tuning(PLE_TUNE_FWD_FB);
     if (fb_env == kBlock || fb_env == 2 * kBlock) pl.FB = fb_env;
     pl.FS = fs;
     pl.G = static_cast<int>((F + fs - 1) / fs);
-    const int wg_env = env_int("PLE_FWD_WG_PER_CU", 0);
+    const int wg_env = tuning(PLE_TUNE_FWD_WG_PER_CU);
     const int64_t target = static_cast<int64_t>(wg_env > 0 ? wg_env : 32) * device_cu_count();
     int64_t c = (target + pl.G - 1) / pl.G;
     if (wg_env <= 0) {
@@ -404,8 +607,16 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
 }
 
 template <int Q, int OUT, int EPI, int VEC>
-hipError_t launch_idx(const FwdArgs &a, int idxb, dim3 grid, size_t lds, hipStream_t s) {
-    // uint8 indices up to 256 bins, int16 beyond (at most 32766 bins)
+hipError_t launch_idx(const FwdArgs &a, int idxb, bool wide, dim3 grid, size_t lds, hipStream_t s) {
+    // uint8 indices up to 256 bins, int16 up to 32768, int32 beyond (those
+    // tables never fit the table kernel's LDS)
+    if (wide) {
+        if (idxb == 1) hipLaunchKernelGGL((ple_fwd_wide_kernel<Q, OUT, EPI, VEC, uint8_t>), grid, dim3(kWideFB), lds, s, a);
+        else if (idxb == 2) hipLaunchKernelGGL((ple_fwd_wide_kernel<Q, OUT, EPI, VEC, int16_t>), grid, dim3(kWideFB), lds, s, a);
+        else hipLaunchKernelGGL((ple_fwd_wide_kernel<Q, OUT, EPI, VEC, int32_t>), grid, dim3(kWideFB), lds, s, a);
+        return hipGetLastError();
+    }
+    if (idxb == 4) return hipErrorInvalidConfiguration;
     if (a.FB == 2 * kBlock) {
         if (idxb == 1) hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, uint8_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
         else hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, int16_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
@@ -417,26 +628,35 @@ hipError_t launch_idx(const FwdArgs &a, int idxb, dim3 grid, size_t lds, hipStre
 }
 
 template <int Q, int OUT, int EPI>
-hipError_t launch_vec(const FwdArgs &a, int vec, int idxb, dim3 grid, size_t lds, hipStream_t s) {
-    // (8 outputs per lane: 16-bit outputs without an epilogue only)
+hipError_t launch_vec(const FwdArgs &a, int vec, int idxb, bool wide, dim3 grid, size_t lds, hipStream_t s) {
+    // (8 outputs per lane: 16-bit outputs without an epilogue, table kernel only)
     if constexpr (OUT != PLE_DTYPE_F32 && EPI == kEpiNone) {
-        if (vec == 8) return launch_idx<Q, OUT, EPI, 8>(a, idxb, grid, lds, s);
+        if (vec == 8 && !wide) {
+            if (a.FB == 2 * kBlock) {
+                if (idxb == 1) hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, 8, uint8_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
+                else hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, 8, int16_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
+            } else {
+                if (idxb == 1) hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, 8, uint8_t, kBlock>), grid, dim3(kBlock), lds, s, a);
+                else hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, 8, int16_t, kBlock>), grid, dim3(kBlock), lds, s, a);
+            }
+            return hipGetLastError();
+        }
     }
-    if (vec == 4) return launch_idx<Q, OUT, EPI, 4>(a, idxb, grid, lds, s);
-    if (vec == 2) return launch_idx<Q, OUT, EPI, 2>(a, idxb, grid, lds, s);
-    return launch_idx<Q, OUT, EPI, 1>(a, idxb, grid, lds, s);
+    if (vec == 4) return launch_idx<Q, OUT, EPI, 4>(a, idxb, wide, grid, lds, s);
+    if (vec == 2) return launch_idx<Q, OUT, EPI, 2>(a, idxb, wide, grid, lds, s);
+    return launch_idx<Q, OUT, EPI, 1>(a, idxb, wide, grid, lds, s);
 }
 
 // Supported (quant, output) pairs: output == quant without an epilogue (the
 // reference operator), output == F32 with one (the fused module tail).
 template <int Q>
-hipError_t launch_q(const FwdArgs &a, int epi, int vec, int idxb, dim3 grid, size_t lds, hipStream_t s) {
+hipError_t launch_q(const FwdArgs &a, int epi, int vec, int idxb, bool wide, dim3 grid, size_t lds, hipStream_t s) {
     switch (epi) {
-        case kEpiBias: return launch_vec<Q, PLE_DTYPE_F32, kEpiBias>(a, vec, idxb, grid, lds, s);
-        case kEpiBiasRelu: return launch_vec<Q, PLE_DTYPE_F32, kEpiBiasRelu>(a, vec, idxb, grid, lds, s);
-        case kEpiLin: return launch_vec<Q, PLE_DTYPE_F32, kEpiLin>(a, vec, idxb, grid, lds, s);
-        case kEpiLinRelu: return launch_vec<Q, PLE_DTYPE_F32, kEpiLinRelu>(a, vec, idxb, grid, lds, s);
-        default: return launch_vec<Q, Q, kEpiNone>(a, vec, idxb, grid, lds, s);
+        case kEpiBias: return launch_vec<Q, PLE_DTYPE_F32, kEpiBias>(a, vec, idxb, wide, grid, lds, s);
+        case kEpiBiasRelu: return launch_vec<Q, PLE_DTYPE_F32, kEpiBiasRelu>(a, vec, idxb, wide, grid, lds, s);
+        case kEpiLin: return launch_vec<Q, PLE_DTYPE_F32, kEpiLin>(a, vec, idxb, wide, grid, lds, s);
+        case kEpiLinRelu: return launch_vec<Q, PLE_DTYPE_F32, kEpiLinRelu>(a, vec, idxb, wide, grid, lds, s);
+        default: return launch_vec<Q, Q, kEpiNone>(a, vec, idxb, wide, grid, lds, s);
     }
 }
 
@@ -464,14 +684,15 @@ int forward_run(const ForwardRequest &r) {
     a.out = r.out; a.idx = r.idx;
     a.N = r.N; a.F = static_cast<int>(r.F); a.B = static_cast<int>(r.B); a.D = static_cast<int>(r.D);
     a.FS = pl.FS; a.G = pl.G; a.C = pl.C; a.NC = pl.NC; a.FB = pl.FB;
+    a.S = pl.S; a.stage_off = pl.stage_off; a.edge_off = pl.edge_off; a.edges_lds = pl.edges_lds;
     const int64_t grid = kNumXcd * tiles_per_xcd(pl.G, pl.C);
     if (grid > INT32_MAX) return PLE_E_TOO_LARGE;
     const int idxb = idx_bytes_for(r.B);
     hipError_t e;
     switch (r.quant) {
-        case PLE_DTYPE_F32: e = launch_q<PLE_DTYPE_F32>(a, epi, pl.vec, idxb, dim3(grid), pl.lds, r.stream); break;
-        case PLE_DTYPE_F16: e = launch_q<PLE_DTYPE_F16>(a, epi, pl.vec, idxb, dim3(grid), pl.lds, r.stream); break;
-        default: e = launch_q<PLE_DTYPE_BF16>(a, epi, pl.vec, idxb, dim3(grid), pl.lds, r.stream); break;
+        case PLE_DTYPE_F32: e = launch_q<PLE_DTYPE_F32>(a, epi, pl.vec, idxb, pl.wide, dim3(grid), pl.lds, r.stream); break;
+        case PLE_DTYPE_F16: e = launch_q<PLE_DTYPE_F16>(a, epi, pl.vec, idxb, pl.wide, dim3(grid), pl.lds, r.stream); break;
+        default: e = launch_q<PLE_DTYPE_BF16>(a, epi, pl.vec, idxb, pl.wide, dim3(grid), pl.lds, r.stream); break;
     }
     return e == hipSuccess ? PLE_OK : static_cast<int>(e);
 }

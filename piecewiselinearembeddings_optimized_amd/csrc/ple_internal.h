@@ -11,8 +11,17 @@
 namespace ple {
 
 constexpr size_t kLdsMax = 160 * 1024;   // LDS per workgroup on gfx950
+// Largest max_n_bins the entry points take (bin indices are int32 beyond
+// 32768 bins, as in the reference; every table offset is 64-bit).
+constexpr int64_t kMaxBins = int64_t{1} << 24;
 
 int device_cu_count();
+
+// Current value of a PLE_TUNE_* planner override (0: the planner's choice).
+int tuning(int knob);
+// Changes whenever a tuning knob is set (plans cached under an older epoch
+// are stale).
+uint32_t tuning_epoch();
 
 inline int idx_bytes_for(int64_t B) { return B <= 256 ? 1 : (B <= 32768 ? 2 : 4); }
 

@@ -19,3 +19,20 @@ def c_oracle():
 
     co.build()
     return co
+
+
+@pytest.fixture
+def tune():
+    """Sets planner overrides (``capi.TUNE`` knobs) for one test; every knob
+    it touched is restored afterwards."""
+    from piecewiselinearembeddings_optimized_amd import capi
+
+    prev = {}
+
+    def set_(knob, value):
+        old = capi.set_tuning(knob, value)
+        prev.setdefault(knob, old)
+
+    yield set_
+    for knob, value in prev.items():
+        capi.set_tuning(knob, value)

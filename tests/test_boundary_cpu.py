@@ -72,6 +72,9 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     args = [dummy] * 5 + [None, dummy, dummy]
     assert lib.ple_forward_launch(*args, 4, 0, 3, 2, 0, 0, None) == -2       # F = 0
     assert lib.ple_forward_launch(*args, 4, 2, 3, 65, 0, 0, None) == -5      # D > 64
+    assert lib.ple_forward_launch(*args, 4, 2, (1 << 24) + 1, 2, 0, 0, None) == -5   # max bins > 2^24
+    assert lib.ple_forward_launch(*args, 0, 2, 40000, 4, 0, 0, None) == 0    # int32 indices: accepted
+    assert lib.ple_forward_launch(*args, 0, 2, 32768, 64, 0, 0, None) == 0   # tables far beyond LDS: accepted
     assert lib.ple_forward_launch(*args, 4, 2, 3, 2, 9, 0, None) == -3       # bad dtype
     assert lib.ple_forward_launch(*args, 0, 2, 3, 2, 0, 0, None) == 0        # empty batch: no launch
     nulls = [None] * 8
@@ -95,6 +98,25 @@ def test_ctypes_binding_declares_the_header_and_maps_errors():
     assert capi.workspace_bytes(0, 2, 3, 4) == 0
     assert capi.workspace_bytes(1024, 8, 48, 24) > 0
     assert capi.workspace_bytes(1024, 8, 48, 65) == 0      # rejected sizes need nothing
+    # tables beyond LDS: the fallback's chunk partials
+    assert capi.workspace_bytes(2048, 4, 40000, 4) >= 4 * 40000 * 2 * 4 * 4
+
+
+def test_tuning_knobs_round_trip():
+    """Planner overrides: set, read back as the previous value, restored;
+    unknown knobs rejected."""
+    from piecewiselinearembeddings_optimized_amd import capi
+
+    L = capi.lib()
+    assert set(capi.TUNE.values()) == set(range(len(capi.TUNE)))
+    header = open(HEADER).read()
+    for name, code in capi.TUNE.items():
+        assert re.search(rf"PLE_TUNE_{name}\s*=\s*{code}\b", header), name
+    for name in capi.TUNE:
+        assert capi.set_tuning(name, 3) == 0
+        assert capi.set_tuning(name, 0) == 3
+    assert L.ple_set_tuning(len(capi.TUNE), 1) == -2
+    assert L.ple_set_tuning(-1, 1) == -2
 
 
 def test_operator_schemas_match_reference():

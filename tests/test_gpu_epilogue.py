@@ -177,9 +177,9 @@ def test_backward_epilogue_lane_group_widths(d, quant, version, relu):
 
 
 @pytest.mark.parametrize("version,relu", [("A", True), ("B", True), ("B", False)])
-def test_fallback_backward_epilogue_matches_oracle(version, relu, monkeypatch):
-    """The shapes that leave the sorted path (PLE_BWD_SIMPLE=1 forces it)."""
-    monkeypatch.setenv("PLE_BWD_SIMPLE", "1")
+def test_fallback_backward_epilogue_matches_oracle(version, relu, tune):
+    """The shapes that leave the sorted path (the BWD_SIMPLE knob forces it)."""
+    tune("BWD_SIMPLE", 1)
     w, w0, b0, g = _setup(0, seed=2)
     (x, e, iw, nb, wt, lw), _, idx, mask = _run_forward(w, w0, b0, version, relu, "f32")
     a = version == "A"

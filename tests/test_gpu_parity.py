@@ -108,33 +108,33 @@ def test_forward_float16_matches_oracle(cfg, c_oracle):
 
 
 @pytest.mark.parametrize("cfg,dtype", [(1, torch.float16), (4, torch.bfloat16)])
-def test_forward_16bit_store_widths_agree(cfg, dtype, monkeypatch):
+def test_forward_16bit_store_widths_agree(cfg, dtype, tune):
     """16-bit outputs store 8 per lane when D allows (16-byte stores) or 4 per
-    lane (PLE_FWD_VEC=4 forces it): the same bits either way."""
+    lane (the FWD_VEC knob forces it): the same bits either way."""
     w = workloads.make(cfg, REDUCED[cfg])
     print(f"forward store widths {w.name} {dtype}", flush=True)
     x, e, iw, nb, wt, bt = _inputs(w)
     out8, idx8 = ops.forward(x, e, iw, nb, wt, dtype)
-    monkeypatch.setenv("PLE_FWD_VEC", "4")
+    tune("FWD_VEC", 4)
     out4, idx4 = ops.forward(x, e, iw, nb, wt, dtype)
-    monkeypatch.delenv("PLE_FWD_VEC")
+    tune("FWD_VEC", 0)
     assert torch.equal(idx8, idx4)
     assert torch.equal(out8.view(torch.int16), out4.view(torch.int16))
 
 
 @pytest.mark.parametrize("cfg", [0, 1, 3, 4])
-def test_forward_workgroup_sizes_agree(cfg, monkeypatch):
-    """256- and 512-thread forward workgroups (PLE_FWD_FB; the planner picks
+def test_forward_workgroup_sizes_agree(cfg, tune):
+    """256- and 512-thread forward workgroups (the FWD_FB knob; the planner picks
     512 for large tables and narrow rows) give the same bits."""
     w = workloads.make(cfg, REDUCED[cfg])
     print(f"forward workgroup sizes {w.name}", flush=True)
     x, e, iw, nb, wt, bt = _inputs(w)
     dtype = torch.bfloat16 if w.quant == "bf16" else torch.float32
     outs = []
-    for fb in ("256", "512"):
-        monkeypatch.setenv("PLE_FWD_FB", fb)
+    for fb in (256, 512):
+        tune("FWD_FB", fb)
         outs.append(ops.forward(x, e, iw, nb, wt, dtype))
-    monkeypatch.delenv("PLE_FWD_FB")
+    tune("FWD_FB", 0)
     assert torch.equal(outs[0][1], outs[1][1])
     assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
 
@@ -332,15 +332,15 @@ def test_two_column_lanes_16bit(d, quant, c_oracle):
 
 
 @pytest.mark.parametrize("d", [10, 30])
-def test_two_column_lanes_match_one_column_lanes(d, c_oracle, monkeypatch):
-    """The one-column-a-lane forms (PLE_FWD_VEC=1, PLE_BWD_VEC=1) at the same
+def test_two_column_lanes_match_one_column_lanes(d, c_oracle, tune):
+    """The one-column-a-lane forms (knobs FWD_VEC=1, BWD_VEC=1) at the same
     even widths: forward bits equal, backward within the fp32 bar of the oracle."""
     w = _random_case(1100, 3, 30, d, seed=d + 11)
     x, e, iw, nb, wt, bt = _inputs(w)
     g = _grad((1100, 3, d), d + 1)
     out2, _ = ops.forward_with_bias(x, e, iw, nb, wt, bt, torch.float32)
-    monkeypatch.setenv("PLE_FWD_VEC", "1")
-    monkeypatch.setenv("PLE_BWD_VEC", "1")
+    tune("FWD_VEC", 1)
+    tune("BWD_VEC", 1)
     out1, idx1 = ops.forward_with_bias(x, e, iw, nb, wt, bt, torch.float32)
     gx, gw, gb = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx1, torch.float32, True, True, True)
     torch.cuda.synchronize()
@@ -349,9 +349,9 @@ def test_two_column_lanes_match_one_column_lanes(d, c_oracle, monkeypatch):
 
 
 @pytest.mark.parametrize("cfg", [1, 3])
-def test_backward_descriptor_buffering_modes_agree(cfg, c_oracle, monkeypatch):
+def test_backward_descriptor_buffering_modes_agree(cfg, c_oracle, tune):
     """One or two LDS buffers for the sorted descriptors (the planner picks by
-    LDS room; PLE_BWD_DBUF forces either): same pieces, same order of every
+    LDS room; the BWD_DBUF knob forces either): same pieces, same order of every
     sum, so bitwise the same gradients, both checked against the oracle."""
     w = workloads.make(cfg, REDUCED[cfg])
     n, f, bmax, d = w.shape
@@ -360,19 +360,19 @@ def test_backward_descriptor_buffering_modes_agree(cfg, c_oracle, monkeypatch):
     _, idx = ops.forward_with_bias(x, e, iw, nb, wt, bt, torch.float32)
     g = _grad((n, f, d), 11)
     res = []
-    for mode in ("0", "1"):
-        monkeypatch.setenv("PLE_BWD_DBUF", mode)
+    for mode in (1, 2):
+        tune("BWD_DBUF", mode)
         res.append(ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, True, True, True))
-    monkeypatch.delenv("PLE_BWD_DBUF")
+    tune("BWD_DBUF", 0)
     for a_, b_ in zip(*res):
         assert torch.equal(a_, b_)
     _check_backward(w, "f32", g, *res[1], c_oracle)
 
 
 @pytest.mark.parametrize("cfg", [0, 1, 2, 3])
-def test_fallback_backward_path_matches_oracle(cfg, c_oracle, monkeypatch):
-    """The simple (non-fused) backward kernels, forced by PLE_BWD_SIMPLE=1."""
-    monkeypatch.setenv("PLE_BWD_SIMPLE", "1")
+def test_fallback_backward_path_matches_oracle(cfg, c_oracle, tune):
+    """The simple (non-fused) backward kernels, forced by the BWD_SIMPLE knob."""
+    tune("BWD_SIMPLE", 1)
     w = workloads.make(cfg, min(REDUCED[cfg] or 4096, 4096))
     n, f, bmax, d = w.shape
     print(f"fallback backward {w.name} shape={w.shape}", flush=True)
