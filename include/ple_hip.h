@@ -55,6 +55,7 @@ enum {
     PLE_E_WORKSPACE = -6,
     PLE_E_UNSUPPORTED = -7,
     PLE_E_MISALIGNED = -8,
+    PLE_E_SCRATCH_LIMIT = -9,
 };
 
 /* Bytes of bin index per (sample, feature) for a given max_n_bins:
@@ -127,6 +128,24 @@ int ple_backward_launch(const void *grad_output, const float *x, const float *bi
                         float *grad_weight, float *grad_bias, int64_t N, int64_t F,
                         int64_t B, int64_t D, int grad_dtype, int quant_dtype,
                         void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * ple_backward_launch without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * workspace is a static device array of PLE_NOALLOC_SCRATCH_BYTES that each
+ * GPU the library runs on holds until the process ends; sizes whose
+ * ple_backward_workspace_bytes exceed it return PLE_E_SCRATCH_LIMIT before
+ * any launch.  Nothing is allocated or freed.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (other streams, other host
+ * threads) race.  Arguments and results as ple_backward_launch.
+ */
+#define PLE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int ple_backward_launch_noalloc(const void *grad_output, const float *x, const float *bin_edges,
+                                const float *inv_bin_widths, const int32_t *n_bins, const float *weight,
+                                const void *bin_indices, float *grad_x, float *grad_weight, float *grad_bias,
+                                int64_t N, int64_t F, int64_t B, int64_t D, int grad_dtype, int quant_dtype,
+                                void *stream);
 
 /*
  * Module epilogue fused into the kernels.  No counterpart in the reference's

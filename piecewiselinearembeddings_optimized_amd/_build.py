@@ -65,7 +65,7 @@ def _hipcc() -> str:
     return p
 
 
-KERNEL_SOURCES = ("ple_capi.hip", "ple_forward.hip", "ple_backward.hip", "ple_encode.hip")
+KERNEL_SOURCES = ("ple_capi.hip", "ple_forward.hip", "ple_backward.hip", "ple_encode.hip", "ple_noalloc.hip")
 
 
 def build_kernels(verbose: bool = False) -> str:

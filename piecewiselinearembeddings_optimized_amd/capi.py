@@ -67,6 +67,8 @@ def lib() -> ctypes.CDLL:
         L.ple_backward_workspace_bytes.restype = sz
         L.ple_backward_launch.argtypes = [p, p, p, p, p, p, p, p, p, p, i64, i64, i64, i64, i32, i32, p, sz, p]
         L.ple_backward_launch.restype = i32
+        L.ple_backward_launch_noalloc.argtypes = [p, p, p, p, p, p, p, p, p, p, i64, i64, i64, i64, i32, i32, p]
+        L.ple_backward_launch_noalloc.restype = i32
         ep = ctypes.POINTER(Epilogue)
         L.ple_forward_epilogue_launch.argtypes = [p, p, p, p, p, ep, p, p, i64, i64, i64, i64, i32, p]
         L.ple_forward_epilogue_launch.restype = i32

@@ -33,6 +33,22 @@ uint32_t tuning_epoch() { return g_tuning_epoch.load(std::memory_order_relaxed);
 
 namespace {
 
+// Zeros n floats (a kernel rather than hipMemsetAsync, so that a caller may
+// capture the launch in a graph).
+__global__ __launch_bounds__(256) void ple_zero_kernel(float *p, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        p[i] = 0.0f;
+}
+
+hipError_t zero_floats(float *p, int64_t n, hipStream_t s) {
+    if (!p || n <= 0) return hipSuccess;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(ple_zero_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, p, n);
+    return hipGetLastError();
+}
+
 int check_common(int64_t N, int64_t F, int64_t B, int64_t D) {
     if (N < 0 || F < 1 || B < 1 || D < 1) return PLE_E_BAD_SHAPE;
     if (F > INT32_MAX / 2 || B > kMaxBins || D > 64) return PLE_E_TOO_LARGE;
@@ -68,6 +84,8 @@ const char *ple_error_string(int code) {
         case PLE_E_WORKSPACE: return "workspace is NULL, too small or not 256-byte aligned";
         case PLE_E_UNSUPPORTED: return "combination not supported (dtype or epilogue pairing)";
         case PLE_E_MISALIGNED: return "pointer misaligned for its element type";
+        case PLE_E_SCRATCH_LIMIT:
+            return "the sizes need more workspace than the no-allocation entry point's static scratch holds";
         default: break;
     }
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
@@ -112,8 +130,8 @@ int ple_backward_launch(const void *grad_output, const float *x, const float *bi
     if (N == 0) {
         // empty batch: the parameter gradients are zero
         hipError_t e = hipSuccess;
-        if (grad_weight) e = hipMemsetAsync(grad_weight, 0, sizeof(float) * F * B * D, s);
-        if (e == hipSuccess && grad_bias) e = hipMemsetAsync(grad_bias, 0, sizeof(float) * F * D, s);
+        if (grad_weight) e = ple::zero_floats(grad_weight, F * B * D, s);
+        if (e == hipSuccess && grad_bias) e = ple::zero_floats(grad_bias, F * D, s);
         return e == hipSuccess ? PLE_OK : static_cast<int>(e);
     }
     if (!grad_output || !x || !bin_edges || !inv_bin_widths || !n_bins || !weight || !bin_indices)
@@ -172,9 +190,9 @@ int ple_backward_epilogue_launch(const float *grad_output, const float *x, const
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (N == 0) {
         hipError_t e = hipSuccess;
-        if (grad_weight) e = hipMemsetAsync(grad_weight, 0, sizeof(float) * F * B * D, s);
-        if (e == hipSuccess && db) e = hipMemsetAsync(db, 0, sizeof(float) * F * D, s);
-        if (e == hipSuccess && grad_lin_weight) e = hipMemsetAsync(grad_lin_weight, 0, sizeof(float) * F * D, s);
+        if (grad_weight) e = ple::zero_floats(grad_weight, F * B * D, s);
+        if (e == hipSuccess && db) e = ple::zero_floats(db, F * D, s);
+        if (e == hipSuccess && grad_lin_weight) e = ple::zero_floats(grad_lin_weight, F * D, s);
         return e == hipSuccess ? PLE_OK : static_cast<int>(e);
     }
     if (!grad_output || !x || !bin_edges || !inv_bin_widths || !n_bins || !weight || !bin_indices)

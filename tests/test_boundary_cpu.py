@@ -57,7 +57,7 @@ def test_host_only_entry_points():
     lib.ple_bin_index_bytes.argtypes = [ctypes.c_int64]
     assert [lib.ple_bin_index_bytes(b) for b in (1, 256, 257, 32768, 32769)] == [1, 1, 2, 2, 4]
     lib.ple_error_string.restype = ctypes.c_char_p
-    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8):
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9):
         assert lib.ple_error_string(code)
     assert lib.ple_abi_version() >> 16 == 1
     assert pkg._C.abi_version() == lib.ple_abi_version()

@@ -1,0 +1,89 @@
+"""The backward entry point that allocates nothing (ple_backward_launch_noalloc).
+
+It runs the same kernels as ple_backward_launch with its workspace in a
+static device array, so its results must equal ple_backward_launch's bit for
+bit -- checked through the C ABI on two calls in a row, the second with a
+smaller input (the array keeps the first call's contents), plus the fp32 bar
+of the float64 oracle, and the rejection of sizes beyond the array.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ple_oracle as po
+from piecewiselinearembeddings_optimized_amd import workloads
+from tests.ple_cases import FP32_ATOL, FP32_RTOL, close_scaled
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+SCRATCH_LIMIT = -9
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _run(w, g, quant_code, noalloc):
+    import piecewiselinearembeddings_optimized_amd  # noqa: F401
+    from piecewiselinearembeddings_optimized_amd import capi
+
+    L = capi.lib()
+    n, f, bmax, d = w.shape
+    x, e, iw, nb, wt = _t(w.x), _t(w.edges), _t(w.inv_widths), _t(w.n_bins), _t(w.weight)
+    qdt = {0: torch.float32, 1: torch.float16, 2: torch.bfloat16}[quant_code]
+    _, idx = torch.ops.rtdl_num_embeddings_cuda.forward(x, e, iw, nb, wt, qdt)
+    gt = _t(g).to(qdt)
+    gx = torch.empty((n, f), device=DEV)
+    gw = torch.empty((f, bmax, d), device=DEV)
+    gb = torch.empty((f, d), device=DEV)
+    s = torch.cuda.current_stream().cuda_stream
+    args = (gt.data_ptr(), x.data_ptr(), e.data_ptr(), iw.data_ptr(), nb.data_ptr(), wt.data_ptr(), idx.data_ptr(),
+            gx.data_ptr(), gw.data_ptr(), gb.data_ptr(), n, f, bmax, d, quant_code, quant_code)
+    if noalloc:
+        rc = L.ple_backward_launch_noalloc(*args, s)
+    else:
+        need = L.ple_backward_workspace_bytes(n, f, bmax, d)
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=DEV)
+        rc = L.ple_backward_launch(*args, ws.data_ptr(), need, s)
+    assert rc == 0, L.ple_error_string(rc)
+    torch.cuda.synchronize()
+    return gx, gw, gb
+
+
+@pytest.mark.parametrize("quant_code", [0, 2])
+def test_noalloc_backward_matches_workspace_backward(quant_code, c_oracle):
+    # first call: c1's recipe at 8192 samples (about 26 MiB of workspace);
+    # second: a smaller input (c0) reusing the array the first call left behind
+    for cfg, n in ((1, 8192), (0, None)):
+        w = workloads.make(cfg, n)
+        nn, f, bmax, d = w.shape
+        print(f"noalloc backward {w.name} shape={w.shape} quant={quant_code}", flush=True)
+        g = np.random.default_rng(cfg + 10 * quant_code).standard_normal((nn, f, d)).astype(np.float32)
+        ref = _run(w, g, quant_code, noalloc=False)
+        got = _run(w, g, quant_code, noalloc=True)
+        for a, b in zip(ref, got):
+            assert torch.equal(a, b)
+        quant = {0: "f32", 2: "bf16"}[quant_code]
+        g_seen = po.quantize(g, quant) if quant != "f32" else g
+        oracle = c_oracle.backward_f64(g_seen, w.x, w.edges, w.inv_widths, w.n_bins, w.weight,
+                                       po.bin_indices(w.x, w.edges, w.n_bins), quant=quant)
+        for name, t, key in (("dx", got[0], "dx"), ("dW", got[1], "dw"), ("db", got[2], "db")):
+            ok, worst = close_scaled(t.cpu().numpy(), oracle[key], oracle[key + "_abs"], FP32_RTOL, FP32_ATOL)
+            print(f"  {name}: worst error / allowance = {worst:.3g}", flush=True)
+            assert ok, name
+
+
+def test_noalloc_rejects_sizes_beyond_its_scratch():
+    from piecewiselinearembeddings_optimized_amd import capi
+
+    L = capi.lib()
+    n, f, bmax, d = 262144, 128, 48, 32          # about 0.5 GiB of workspace
+    assert L.ple_backward_workspace_bytes(n, f, bmax, d) > 64 << 20
+    dummy = 256
+    rc = L.ple_backward_launch_noalloc(*([dummy] * 7), dummy, dummy, dummy, n, f, bmax, d, 0, 0, None)
+    assert rc == SCRATCH_LIMIT
+    assert b"static scratch" in L.ple_error_string(rc)
