@@ -230,11 +230,10 @@ int ple_encode_backward_launch(const float *grad_output, const float *x, const f
  *   PLE_TUNE_FWD_WIDE       1: the wide-table forward kernel for any shape
  *   PLE_TUNE_BWD_SIMPLE     1: the fallback backward kernels for any shape
  *   PLE_TUNE_BWD_SIMPLE_GLOBAL 1: their histogram cells in global memory
- *   PLE_TUNE_BWD_VEC        gradient floats per lane (1 or 8)
+ *   PLE_TUNE_BWD_VEC        1: one gradient element per lane
  *   PLE_TUNE_BWD_FS         features per backward sub-tile (1, 2, 4, 8, 16)
- *   PLE_TUNE_BWD_RB         reduce workgroup size (256 or 512 threads)
- *   PLE_TUNE_BWD_DBUF       sub-tile descriptor buffers in LDS (1 or 2)
- *   PLE_TUNE_BWD_WG_PER_CU  reduce workgroups per CU
+ *   PLE_TUNE_BWD_RB         reducer threads per backward workgroup (256 or 512)
+ *   PLE_TUNE_BWD_WG_PER_CU  backward workgroups per CU
  * A forced value the shape cannot take is ignored.  Returns the knob's
  * previous value, or PLE_E_BAD_SHAPE for an unknown knob.  Not synchronised
  * with launches running on other threads.
@@ -250,9 +249,8 @@ enum {
     PLE_TUNE_BWD_VEC = 7,
     PLE_TUNE_BWD_FS = 8,
     PLE_TUNE_BWD_RB = 9,
-    PLE_TUNE_BWD_DBUF = 10,
-    PLE_TUNE_BWD_WG_PER_CU = 11,
-    PLE_TUNE_COUNT = 12,
+    PLE_TUNE_BWD_WG_PER_CU = 10,
+    PLE_TUNE_COUNT = 11,
 };
 int ple_set_tuning(int knob, int value);
 

@@ -14,31 +14,30 @@
 //             d lin_w[f] = sum_n g x, d lin_b[f] = sum_n g (in db's slot)
 // dx and dW use g_ple rounded through the quantisation dtype.
 //
-// Main path: two kernels over tiles of P (sample, feature) pairs (NT samples
-// x FS features, "sub-tiles").
+// Main path: ple_bwd_fused_kernel, over tiles of P (sample, feature) pairs
+// (NT samples x FS features, "sub-tiles").  One workgroup per feature group
+// and chunk of SPC sub-tiles: four (or eight) reducer waves and one sorter
+// wave, which sorts sub-tile t + 1 into one LDS buffer while the reducers
+// reduce sub-tile t from the other.
 //
-// ple_bwd_sort_kernel -- one workgroup per sub-tile.  Reads the bin index and
-//   x of every pair, computes q(frac) and the edge flag, and counting-sorts
-//   the pairs by (feature, bin): per 64-pair block, ranks of equal keys from
-//   64-bit ballots, a per-key prefix over blocks and a block-wide scan over
-//   keys -- deterministic and stable.  Writes the sorted row descriptors
-//   {q(frac) (-0 marks x on the bin's left edge), sample | feature << 24} and
-//   the sub-tile's pieces: every (feature, bin) run of sorted rows cut into
-//   pieces of kL rows.
+// sorter -- reads the bin index and x of every pair, computes q(frac) and the
+//   edge flag, and counting-sorts the pairs by (feature, bin): per 64-pair
+//   block, ranks of equal keys from 64-bit ballots plus the key's running
+//   count, then a wave scan over the keys -- deterministic and stable.
+//   Writes the sorted row descriptors {q(frac) (-0 marks x on the bin's left
+//   edge), sample | feature << 24} and the sub-tile's pieces: every (feature,
+//   bin) run of sorted rows cut into pieces of kL rows.  Nothing leaves LDS.
 //
-// ple_bwd_reduce_kernel -- one workgroup per feature group and chunk of
-//   sub-tiles; nothing but the gradient stream and LDS work.  Lane groups
+// reducers -- nothing but the gradient stream and LDS work.  Lane groups
 //   (D/VEC lanes, one grad_output row per step) take equal runs of pieces:
 //   each row is read once, its dx is the lane group's DPP-reduced dot with
 //   the LDS weight row (kept in LDS at its sorted position), and bucket /
 //   weighted / bias sums run in registers until the key changes (checked
-//   once per piece).  A run's first key goes to a per-run record, every
-//   later key straight into the LDS histogram (no other run can own it); the
+//   once per piece).  A run's first key goes to a per-run record, every later
+//   key straight into the LDS histogram (no other run can own it); the
 //   records are added run by run in order.  Each row's dx is staged in LDS
 //   at its pair's position (the descriptor names it) and leaves
-//   feature-major in whole lines.  The
-//   next sub-tile's descriptors travel while the current one is reduced.
-//   The chunk's histogram is written once.
+//   feature-major in whole lines.  The chunk's histogram is written once.
 //
 // ple_bwd_dx_transpose_kernel turns the feature-major dx into [N, F];
 // ple_bwd_chunksum_kernel adds the chunk partials in chunk order;
@@ -73,9 +72,6 @@ struct BwdArgs {
     float *db;
     float *part;     // [Cd][F][B][2D] chunk partials {bucket | weighted}
     float *part_db;  // [Cd][F][D] chunk partials of the bias gradient
-    uint2 *desc;     // [T][G][P] sorted row descriptors {q(frac) (-0: edge row), sample | fl << 24}
-    uint32_t *piece; // [T][G][PM] pieces {bin | fl << 12 | first row << 16 | (rows - 1) << 28}
-    int *npc;        // [T][G] pieces per sub-tile
     float *dxt;      // [F][N] dx, feature-major (transposed into dx at the end)
     const uint32_t *mask;   // [N][F][MW] ReLU pass bits of the forward (epilogue with ReLU)
     const float *lin_w;     // [F][D] linear0 weight (version-B epilogue)
@@ -90,50 +86,17 @@ struct BwdArgs {
     int db_from_buckets;   // finalize: db = sum of the bin buckets (no raw-gradient partials)
     int fin_direct;        // finalize: chunk sums read straight from the partials (no LDS table)
     int fin_summed;        // finalize: the chunk partials are summed into chunk 0 already
-    int dbuf;              // reduce: two LDS buffers for the sub-tile descriptors
+    int idxb;              // bytes per bin index (1 or 2 on the sorted path)
     // sorted path
-    int FS, G, NT, T, SPC, PM, LGW, nbits;   // T sub-tiles, SPC sub-tiles per chunk, PM piece capacity
-    int so_nb, so_edge, so_iw, so_cnt, so_seg, so_tmp, so_desc, so_piece;   // sort LDS
+    int FS, G, NT, T, SPC, PM, LGW;   // T sub-tiles, SPC sub-tiles per chunk, PM piece capacity
     int ro_qw, ro_hist, ro_db, ro_iw, ro_nb, ro_desc, ro_piece, ro_npc, ro_rec, ro_rkey, ro_rfl, ro_dx,
-        ro_lw, ro_dlw;   // reduce LDS
+        ro_lw, ro_dlw, ro_edge, ro_cnt, ro_seg, ro_tmp;   // fused kernel LDS
 };
 
-// Exclusive prefix sum of a[0..n) in place, all kBlock threads.
-__device__ void block_exclusive_scan(int *a, int n, int *tmp) {
-    const int tid = threadIdx.x;
-    const int lane = tid % kWave;
-    const int wv = tid / kWave;
-    const int per = (n + kBlock - 1) / kBlock;
-    const int b0 = min(n, tid * per);
-    const int b1 = min(n, b0 + per);
-    int local = 0;
-    for (int i = b0; i < b1; ++i) local += a[i];
-    int v = local;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const int t = __shfl_up(v, off);
-        if (lane >= off) v += t;
-    }
-    if (lane == kWave - 1) tmp[wv] = v;
-    __syncthreads();
-    int run = v - local;
-    for (int w = 0; w < wv; ++w) run += tmp[w];
-    for (int i = b0; i < b1; ++i) {
-        const int t = a[i];
-        a[i] = run;
-        run += t;
-    }
-    __syncthreads();
-}
-
 constexpr int kP = 1024;                        // (sample, feature) pairs per sub-tile
-constexpr int kPairsPerThread = kP / kBlock;
-constexpr int kMaxBlocksPerFeature = kP / kWave;   // 64-pair blocks per sub-tile (a multiple of 8)
 // Rows per piece: every (feature, bin) run of a sorted sub-tile is cut into
 // pieces of kL consecutive rows (the last one shorter).
 constexpr int kL = 4;
-// Piece capacity per sub-tile: at most P / kL + (non-empty keys) pieces.
-constexpr int kMaxPieces = kP / kL + kP;
 
 // backward epilogue flags (template argument of the reduce kernel)
 // Reduce workgroups of twice the usual size: where LDS leaves room for only
@@ -144,164 +107,188 @@ constexpr int kBwdRelu = 1;
 constexpr int kBwdLin = 2;
 
 // ---------------------------------------------------------------------------
-// sort
+// sub-tile sort (all threads of the fused kernel, between reduce phases)
 // ---------------------------------------------------------------------------
 
-template <int Q, typename IdxT>
-__global__ __launch_bounds__(kBlock) void ple_bwd_sort_kernel(BwdArgs a) {
-    extern __shared__ __align__(16) unsigned char lds[];
-    const int FS = a.FS, B = a.B, F = a.F, NT = a.NT;
-    const int KB = B + 1;                   // keys per feature; key B marks padding rows
-    int *s_nb = reinterpret_cast<int *>(lds + a.so_nb);                 // [FS]
-    float *s_edge = reinterpret_cast<float *>(lds + a.so_edge);         // [FS][B+1]
-    float *s_iw = reinterpret_cast<float *>(lds + a.so_iw);             // [FS][B]
-    uint16_t *s_cnt = reinterpret_cast<uint16_t *>(lds + a.so_cnt);     // [P/64][FS*(B+1)]
-    int *s_seg = reinterpret_cast<int *>(lds + a.so_seg);               // [FS*(B+1)] {start | first piece << 16}
-    int *s_tmp = reinterpret_cast<int *>(lds + a.so_tmp);               // [kWavesPerBlock]
-    uint2 *s_sdesc = reinterpret_cast<uint2 *>(lds + a.so_desc);        // [P]
-    uint32_t *s_piece = reinterpret_cast<uint32_t *>(lds + a.so_piece); // [PM]
+constexpr int kBlocks = kP / kWave;   // 64-pair blocks of a sub-tile
 
-    int g, t;
-    if (!decode_tile(blockIdx.x, a.G, a.T, g, t)) return;
-    const int f0 = g * FS;
-    const int nfh = min(FS, F - f0);
-    const int64_t sub = static_cast<int64_t>(t) * NT;
-    const int ns = static_cast<int>(min(static_cast<int64_t>(NT), a.N - sub));
-    const int tid = threadIdx.x;
-    const int lane = tid % kWave;
-
-    // Pairs in sample-major order, p = s * FS + fl (FS and NT are powers of
-    // two: shifts instead of divisions), so a wave's loads of x and the bin
-    // indices cover whole runs of each sample's features.  Thread tid holds
-    // pairs p = tid + u * kBlock: each wave's lanes hold a 64-pair block and
-    // rank it among themselves without going through LDS.  Keys are
-    // fl * KB + bin (bin B marks padding).  Unconditional loads (pair 0
-    // stands in for padding).
+// Bin index and x of this thread's pairs of sub-tile t: pairs p = tid + u RB
+// in sample-major order (p = s * FS + fl), so a load instruction covers whole
+// runs of each sample's features.  Pairs outside the batch or the feature
+// range read pair 0 (ignored when sorted).
+template <int RB, typename IdxT>
+__device__ __forceinline__ void tile_load(const BwdArgs &a, int t, int f0, int nfh, int tid, int (&pk)[kP / RB],
+                                          float (&pv)[kP / RB]) {
+    const int FS = a.FS;
     const int fs_shift = __ffs(FS) - 1;
-    const int NK = FS * KB;                           // keys of the sub-tile
-    const int kbits = 32 - __clz(NK - 1);             // bits of a key (NK >= 2)
-    int pk[kPairsPerThread];
-    float pv[kPairsPerThread];
+    const int64_t sub = static_cast<int64_t>(t) * a.NT;
+    const int ns = static_cast<int>(min(static_cast<int64_t>(a.NT), a.N - sub));
 #pragma unroll
-    for (int u = 0; u < kPairsPerThread; ++u) {
-        const int p = tid + u * kBlock;
+    for (int u = 0; u < kP / RB; ++u) {
+        const int p = tid + u * RB;
         const int s = p >> fs_shift;
         const int fl = p & (FS - 1);
-        const int64_t pair = (s < ns && fl < nfh) ? (sub + s) * F + f0 + fl : 0;
+        const int64_t pair = (s < ns && fl < nfh) ? (sub + s) * a.F + f0 + fl : 0;
         pk[u] = load_idx<IdxT>(a.idx, pair);
         pv[u] = a.x[pair];
     }
-    for (int i = tid; i < FS; i += kBlock) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
-    // (rows past the last feature are never read: their pairs are padding)
-    for (int i = tid; i < FS * KB; i += kBlock)
-        s_edge[i] = i < nfh * KB ? a.edges[static_cast<int64_t>(f0) * KB + i] : 0.0f;
-    for (int i = tid; i < FS * B; i += kBlock)
-        s_iw[i] = i < nfh * B ? a.iw[static_cast<int64_t>(f0) * B + i] : 0.0f;
-    for (int i = tid; i < (kP / kWave) * NK; i += kBlock) s_cnt[i] = 0;
-    __syncthreads();
+}
 
-    // A. per pair: key, edge flag, q(frac); its rank among the equal keys of
-    //    its block from 64-bit ballots (the wave64 "match-any"); the block's
-    //    first pair of each key writes the key's count
-    int pkey[kPairsPerThread];      // key | edge << 16
-    uint32_t pq[kPairsPerThread];
-    int prank[kPairsPerThread];
-    const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+// Counting sort of sub-tile t's pairs by key (feature, bin) = fl * B + bin,
+// stable and deterministic, by all RB threads, in two parts:
+// tile_rank (A), then -- after a barrier -- tile_place (B, C):
+//   A. per pair: bin, q(frac) and the edge flag; its rank among the equal
+//      keys of its 64-pair block (64-bit ballots over the bin bits within the
+//      lanes of its feature -- a lane's feature is the same in every block);
+//      the block's first pair of each key stores the key's count in the block
+//      (s_cnt, zero beforehand).  Per pair key | rank << 16 and the q(frac)
+//      bits stay in registers.
+//   B. per key (each thread a contiguous run of keys): the exclusive prefix
+//      of its block counts in place, then a scan over the keys gives every key
+//      its first row and first piece (pieces: the key's rows cut into runs of
+//      kL) in s_seg, with the totals in s_seg[NK];
+//   C. scatter: row descriptor {q(frac) bits (-0: x on the bin's left edge,
+//      k >= 1; a real -0 is stored as +0), sample | fl << 24} at its sorted
+//      position, and the piece entry {bin | fl << 12 | first row << 16 |
+//      (rows - 1) << 28} from each piece's first row.
+// Pairs outside the batch or feature range take key NK and are not stored.
+// The caller synchronises between the parts, before the descriptors are
+// read, and before s_cnt is cleared for a later sort.
+template <int Q, int RB>
+__device__ __forceinline__ void tile_rank(const BwdArgs &a, int t, int nfh, int tid, const int (&pk)[kP / RB],
+                                          const float (&pv)[kP / RB], const int *s_nb, const float *s_edge,
+                                          const float *s_iw, uint16_t *s_cnt, int (&ko)[kP / RB],
+                                          uint32_t (&qb)[kP / RB]) {
+    constexpr int kPR = kP / RB;
+    const int FS = a.FS, B = a.B, NT = a.NT;
+    const int fs_shift = __ffs(FS) - 1;
+    const int ns = static_cast<int>(min(static_cast<int64_t>(NT), a.N - static_cast<int64_t>(t) * NT));
+    const int NK = FS * B;                       // keys; NK marks padding
+    const int lane = tid & (kWave - 1);
+    const int fl = lane & (FS - 1);              // this thread's feature in every block
+    const bool f_ok = fl < nfh;
+    const int kb = 32 - __clz(B);                // bits of a bin in [0, B]
+    // lanes of this lane's feature: those equal to it in the low log2(FS) bits
+    unsigned long long flm = ~0ull;
+    {
+        constexpr unsigned long long kPat[6] = {0xAAAAAAAAAAAAAAAAull, 0xCCCCCCCCCCCCCCCCull, 0xF0F0F0F0F0F0F0F0ull,
+                                                0xFF00FF00FF00FF00ull, 0xFFFF0000FFFF0000ull, 0xFFFFFFFF00000000ull};
 #pragma unroll
-    for (int u = 0; u < kPairsPerThread; ++u) {
-        const int p = tid + u * kBlock;
+        for (int i = 0; i < 6; ++i)
+            if ((1 << i) < FS) flm &= ((fl >> i) & 1) ? kPat[i] : ~kPat[i];
+    }
+    const int n = s_nb[fl];
+    const float *erow = s_edge + fl * (B + 1);
+    const float *irow = s_iw + fl * B;
+    const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+
+    // A. keys and ranks: key | rank << 16 (keys below 2^16, ranks below 64)
+#pragma unroll
+    for (int u = 0; u < kPR; ++u) {
+        const int p = tid + u * RB;
         const int s = p >> fs_shift;
-        const int fl = p & (FS - 1);
-        int k = B, edge = 0;
-        float qf = 0.0f;
-        if (s < ns && fl < nfh) {
-            k = clamp_bin(pk[u], s_nb[fl]);
-            const float v = pv[u];
-            const float e = s_edge[fl * KB + k];
-            qf = quant<Q>((v - e) * s_iw[fl * B + k]);
-            edge = k > 0 && v == e;
-        }
-        const int key = fl * KB + k;
-        pkey[u] = key | (edge << 16);
-        pq[u] = __float_as_uint(qf);
-        unsigned long long m = ~0ull;
-        for (int bit = 0; bit < kbits; ++bit) {
-            const bool set = (key >> bit) & 1;
+        const bool valid = f_ok && s < ns;
+        const int k = clamp_bin(pk[u], n);
+        const float v = pv[u];
+        const float e = erow[k];
+        const uint32_t q = __float_as_uint(quant<Q>((v - e) * irow[k]));
+        // x on e_k (k >= 1) gives q(frac) == +0 exactly; such rows carry -0
+        // instead, which marks the edge term and adds the same zero
+        qb[u] = (k > 0 && v == e) ? 0x80000000u : (q == 0x80000000u ? 0u : q);
+        const int kk = valid ? k : B;
+        unsigned long long m = flm;
+        for (int bit = 0; bit < kb; ++bit) {
+            const bool set = (kk >> bit) & 1;
             const unsigned long long bal = __ballot(set);
             m &= set ? bal : ~bal;
         }
         const int rank = __popcll(m & lt);
-        prank[u] = rank;
-        if (rank == 0) s_cnt[(p / kWave) * NK + key] = static_cast<uint16_t>(__popcll(m));
+        const int key = valid ? fl * B + k : NK;
+        if (rank == 0 && key < NK) s_cnt[(p >> 6) * NK + key] = static_cast<uint16_t>(__popcll(m));
+        ko[u] = key | (rank << 16);
+    }
+}
+
+template <int RB>
+__device__ __forceinline__ void tile_place(const BwdArgs &a, int tid, const int (&ko)[kP / RB],
+                                           const uint32_t (&qb)[kP / RB], uint16_t *s_cnt, int *s_seg, int *s_tmp,
+                                           uint2 *desc, uint32_t *piece, int *npc) {
+    constexpr int kPR = kP / RB;
+    const int FS = a.FS, B = a.B;
+    const int fs_shift = __ffs(FS) - 1;
+    const int NK = FS * B;
+    const int lane = tid & (kWave - 1);
+    const int wv = tid / kWave;
+    const int fl = lane & (FS - 1);
+
+    // B. per key: block prefixes in place, then the scan over keys (rows in
+    //    the low half, pieces in the high half; both below 2^16)
+    const int kpt = (NK + RB - 1) / RB;
+    const int j0 = min(NK, tid * kpt);
+    const int j1 = min(NK, j0 + kpt);
+    int local = 0;
+    for (int j = j0; j < j1; ++j) {
+        uint16_t *col = s_cnt + j;
+        int cc[kBlocks];
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) cc[b] = col[b * NK];
+        int run = 0;
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) {
+            col[b * NK] = static_cast<uint16_t>(run);
+            run += cc[b];
+        }
+        s_seg[j] = run;
+        local += run | (((run + kL - 1) / kL) << 16);
+    }
+    int incl = local;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+    }
+    if (lane == kWave - 1) s_tmp[wv] = incl;
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < RB / kWave; ++w) {
+        const int tw = s_tmp[w];
+        before += w < wv ? tw : 0;
+        total += tw;
+    }
+    int run = before + incl - local;
+    for (int j = j0; j < j1; ++j) {
+        const int c = s_seg[j];
+        s_seg[j] = run;
+        run += c | (((c + kL - 1) / kL) << 16);
+    }
+    if (tid == 0) {
+        s_seg[NK] = total;
+        *npc = total >> 16;
     }
     __syncthreads();
 
-    // C. per key: exclusive prefix of its counts over the blocks (held in
-    //    registers), then {count | pieces << 16} for the scan
-    for (int kk = tid; kk < NK; kk += kBlock) {
-        uint16_t *col = s_cnt + kk;
-        int run = 0;
-        // eight blocks' counts in flight at a time (registers)
-        for (int b0 = 0; b0 < kMaxBlocksPerFeature; b0 += 8) {
-            int cc[8];
+    // C. scatter
 #pragma unroll
-            for (int bb = 0; bb < 8; ++bb) cc[bb] = col[(b0 + bb) * NK];
-#pragma unroll
-            for (int bb = 0; bb < 8; ++bb) {
-                col[(b0 + bb) * NK] = static_cast<uint16_t>(run);
-                run += cc[bb];
+    for (int u = 0; u < kPR; ++u) {
+        const int key = ko[u] & 0xffff;
+        if (key < NK) {
+            const int p = tid + u * RB;
+            const int s = p >> fs_shift;
+            const int st = s_seg[key];
+            const int within = s_cnt[(p >> 6) * NK + key] + (ko[u] >> 16);
+            const int slot = (st & 0xffff) + within;
+            desc[slot] = make_uint2(qb[u], static_cast<uint32_t>(s) | (static_cast<uint32_t>(fl) << 24));
+            if (within % kL == 0) {
+                const int cnt = (s_seg[key + 1] & 0xffff) - (st & 0xffff);
+                const int rows = min(kL, cnt - within);
+                piece[(st >> 16) + within / kL] = static_cast<uint32_t>(key - fl * B) |
+                                                  (static_cast<uint32_t>(fl) << 12) |
+                                                  (static_cast<uint32_t>(slot) << 16) |
+                                                  (static_cast<uint32_t>(rows - 1) << 28);
             }
         }
-        // padding rows (bin B of a feature): no pieces.  (kk % KB without a
-        // division: FS <= 16)
-        int k = kk;
-        while (k >= KB) k -= KB;
-        const int pieces = k < B ? (run + kL - 1) / kL : 0;
-        s_seg[kk] = run | (pieces << 16);
     }
-    __syncthreads();
-    // run starts (low half) and first piece of each run (high half); neither
-    // sum reaches 2^16
-    block_exclusive_scan(s_seg, NK, s_tmp);
-
-    // D. scatter: sorted position -> row descriptor; the first row of every
-    //    piece writes the piece's entry
-#pragma unroll
-    for (int u = 0; u < kPairsPerThread; ++u) {
-        const int p = tid + u * kBlock;
-        const int s = p >> fs_shift;
-        const int fl = p & (FS - 1);
-        const int key = pkey[u] & 0xffff;
-        const int k = key - fl * KB;
-        const int sg = s_seg[key];
-        const int within = s_cnt[(p / kWave) * NK + key] + prank[u];
-        const int slot = (sg & 0xffff) + within;
-        // x on e_k (k >= 1) gives q(frac) == +0 exactly; such rows carry -0
-        // instead, which marks the edge term and adds the same zero.  A -0
-        // from anywhere else becomes +0 (the same contribution).
-        uint32_t qbits = pq[u];
-        qbits = (pkey[u] >> 16) ? 0x80000000u : (qbits == 0x80000000u ? 0u : qbits);
-        s_sdesc[slot] = make_uint2(qbits, static_cast<uint32_t>(s) | (static_cast<uint32_t>(fl) << 24));
-        if (k < B && within % kL == 0) {
-            // the run ends where the next key's (at least the padding key B) begins
-            const int end = s_seg[key + 1] & 0xffff;
-            const int rows = min(kL, end - slot);
-            s_piece[(sg >> 16) + within / kL] = static_cast<uint32_t>(k) | (static_cast<uint32_t>(fl) << 12) |
-                                                (static_cast<uint32_t>(slot) << 16) |
-                                                (static_cast<uint32_t>(rows - 1) << 28);
-        }
-    }
-    __syncthreads();
-
-    // out: descriptors (16-byte stores), pieces, piece count
-    const int64_t tile = static_cast<int64_t>(t) * a.G + g;
-    uint4 *ddst = reinterpret_cast<uint4 *>(a.desc + tile * kP);
-    const uint4 *dsrc = reinterpret_cast<const uint4 *>(s_sdesc);
-    for (int i = tid; i < kP / 2; i += kBlock) ddst[i] = dsrc[i];
-    const int npc = s_seg[FS * KB - 1] >> 16;     // the last key is padding: no pieces of its own
-    uint32_t *pdst = a.piece + tile * a.PM;
-    for (int i = tid; i < npc; i += kBlock) pdst[i] = s_piece[i];
-    if (tid == 0) a.npc[tile] = npc;
 }
 
 // ---------------------------------------------------------------------------
@@ -309,7 +296,8 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_sort_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 
 template <int GD, int Q, int VEC, int LGW_T, int EPI, int RB>
-__global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
+__global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
+    constexpr int NTH = RB;
     constexpr bool kRelu = (EPI & kBwdRelu) != 0;
     constexpr bool kLin = (EPI & kBwdLin) != 0;
     // With fp32 rounding and no linear0 branch the bias gradient is the sum of
@@ -323,9 +311,13 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
     float *s_db = reinterpret_cast<float *>(lds + a.ro_db);             // [FS][D]
     float *s_iw = reinterpret_cast<float *>(lds + a.ro_iw);             // [FS][B]
     int *s_nb = reinterpret_cast<int *>(lds + a.ro_nb);                 // [FS]
-    uint2 *s_sdesc = reinterpret_cast<uint2 *>(lds + a.ro_desc);        // [1|2][P+1]: sorted rows, then a dummy row
-    uint32_t *s_piece = reinterpret_cast<uint32_t *>(lds + a.ro_piece); // [1|2][PM]
-    int *s_npc = reinterpret_cast<int *>(lds + a.ro_npc);               // [1|2]
+    uint2 *s_sdesc = reinterpret_cast<uint2 *>(lds + a.ro_desc);        // [P+1]: sorted rows, then a dummy row
+    uint32_t *s_piece = reinterpret_cast<uint32_t *>(lds + a.ro_piece); // [PM]
+    int *s_npc = reinterpret_cast<int *>(lds + a.ro_npc);               // [1]
+    float *s_edge = reinterpret_cast<float *>(lds + a.ro_edge);         // [FS][B+1] (sort)
+    uint16_t *s_cnt = reinterpret_cast<uint16_t *>(lds + a.ro_cnt);     // [2][P/64][FS*B] block counts (sort)
+    int *s_seg = reinterpret_cast<int *>(lds + a.ro_seg);               // [FS*B+1] key starts (sort)
+    int *s_tmp = reinterpret_cast<int *>(lds + a.ro_tmp);               // [RB/64] (sort)
     float *s_rec = reinterpret_cast<float *>(lds + a.ro_rec);           // [LG][RS]
     int *s_rkey = reinterpret_cast<int *>(lds + a.ro_rkey);             // [LG]
     int *s_rfl = reinterpret_cast<int *>(lds + a.ro_rfl);               // [LG]
@@ -343,57 +335,50 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
     const int tid = threadIdx.x;
     const int PM = a.PM;
 
-    // The next sub-tile's descriptors, pieces and piece count travel in
-    // registers while the current one is reduced (kP / 2 / RB uint4 of
-    // descriptors per thread; kPieceRegsRB piece entries, the ones past the
-    // capacity re-read entry 0 and are never stored).
-    // (named registers, not arrays: a loop over a register array that is not
-    // unrolled would put it in scratch memory)
-    constexpr int kDescRegs = kP / 2 / RB;
-    constexpr int kPieceRegsRB = (kMaxPieces + RB - 1) / RB;
-    static_assert(kDescRegs * 2 * RB == kP && kDescRegs <= 2 && kPieceRegsRB >= 3 && kPieceRegsRB <= 5,
-                  "prefetch registers");
-    uint4 pd0, pd1 = make_uint4(0u, 0u, 0u, 0u);
-    uint32_t pp0, pp1, pp2, pp3 = 0, pp4 = 0;
-    int pnpc;
-#define PLE_PREFETCH(T_)                                                                         \
-    do {                                                                                         \
-        const int64_t tile_ = static_cast<int64_t>(T_) * a.G + g;                                \
-        const uint4 *src_ = reinterpret_cast<const uint4 *>(a.desc + tile_ * kP);                \
-        pd0 = src_[tid];                                                                         \
-        if constexpr (kDescRegs > 1) pd1 = src_[tid + RB];                                       \
-        const uint32_t *ps_ = a.piece + tile_ * PM;                                              \
-        pp0 = ps_[tid < PM ? tid : 0];                                                           \
-        pp1 = ps_[tid + RB < PM ? tid + RB : 0];                                                 \
-        pp2 = ps_[tid + 2 * RB < PM ? tid + 2 * RB : 0];                                         \
-        if constexpr (kPieceRegsRB > 3) pp3 = ps_[tid + 3 * RB < PM ? tid + 3 * RB : 0];         \
-        if constexpr (kPieceRegsRB > 4) pp4 = ps_[tid + 4 * RB < PM ? tid + 4 * RB : 0];         \
-        pnpc = a.npc[tile_];                                                                     \
-    } while (0)
-    PLE_PREFETCH(t_begin);
+    // the sort's pairs of the next sub-tile (bin index, x), loaded a sub-tile
+    // ahead; bin indices are uint8 or int16 here (at most 4096 bins)
+    int pk[kP / RB];
+    float pv[kP / RB];
+    auto load_pairs = [&](int t) __attribute__((always_inline)) {
+        if (a.idxb == 1) tile_load<RB, uint8_t>(a, t, f0, nfh, tid, pk, pv);
+        else tile_load<RB, int16_t>(a, t, f0, nfh, tid, pk, pv);
+    };
+    load_pairs(t_begin);
+    // the sort's block counts start at zero: two buffers, one for the sort in
+    // progress, one cleared for the sort after it (dwords: two counts each)
+    const int NK = FS * B;
+    const int cnt_half = ((kBlocks * NK + 1) / 2) * 2;        // counts per buffer (even)
+    auto clear_counts = [&](int bsel) __attribute__((always_inline)) {
+        uint32_t *w = reinterpret_cast<uint32_t *>(s_cnt + bsel * cnt_half);
+        for (int i = tid; i < cnt_half / 2; i += NTH) w[i] = 0u;
+    };
+    int ko[kP / RB];          // the next sub-tile's keys | ranks, and q(frac) bits
+    uint32_t qb[kP / RB];
 
     // ---- stage tables, clear accumulators ---------------------------------
-    // Rows past a piece's end read the dummy row kP of their buffer: q(frac) = +0 and sample
+    // Rows past a piece's end read the dummy row kP: q(frac) = +0 and sample
     // NT, whose gradient offset lies past every sub-tile's span (zeros).
-    if (tid == 0) {
-        s_sdesc[kP] = make_uint2(0u, static_cast<uint32_t>(NT));
-        if (a.dbuf) s_sdesc[2 * kP + 1] = make_uint2(0u, static_cast<uint32_t>(NT));
-    }
-    for (int i = tid; i < FS; i += RB) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
-    for (int i = tid; i < FS * B; i += RB) {
+    if (tid == 0) s_sdesc[kP] = make_uint2(0u, static_cast<uint32_t>(NT));
+    clear_counts(0);
+    clear_counts(1);
+    for (int i = tid; i < FS; i += NTH) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
+    for (int i = tid; i < FS * B; i += NTH) {
         const int fl = i / B;
         s_iw[i] = fl < nfh ? a.iw[static_cast<int64_t>(f0) * B + i] : 0.0f;
     }
-    for (int i = tid; i < FS * B * 2 * D; i += RB) s_hist[i] = 0.0f;
-    for (int i = tid; i < FS * D; i += RB) s_db[i] = 0.0f;
+    // (rows past the last feature are never read: their pairs are padding)
+    for (int i = tid; i < FS * (B + 1); i += NTH)
+        s_edge[i] = i < nfh * (B + 1) ? a.edges[static_cast<int64_t>(f0) * (B + 1) + i] : 0.0f;
+    for (int i = tid; i < FS * B * 2 * D; i += NTH) s_hist[i] = 0.0f;
+    for (int i = tid; i < FS * D; i += NTH) s_db[i] = 0.0f;
     if constexpr (kLin) {
-        for (int i = tid; i < FS * D; i += RB) {
+        for (int i = tid; i < FS * D; i += NTH) {
             s_lw[i] = i / D < nfh ? a.lin_w[static_cast<int64_t>(f0) * D + i] : 0.0f;
             s_dlw[i] = 0.0f;
         }
     }
     __syncthreads();
-    for (int i = tid; i < FS * B * D; i += RB) {
+    for (int i = tid; i < FS * B * D; i += NTH) {
         const int fl = i / (B * D);
         const int r = i - fl * (B * D);
         const int k = r / D;
@@ -405,6 +390,14 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
         }
         s_qw[i] = w;
     }
+
+    // the first sub-tile's sort (the tables it reads are staged before the
+    // barrier above), then the next sub-tile's pairs
+    tile_rank<Q, RB>(a, t_begin, nfh, tid, pk, pv, s_nb, s_edge, s_iw, s_cnt, ko, qb);
+    __syncthreads();
+    tile_place<RB>(a, tid, ko, qb, s_cnt, s_seg, s_tmp, s_sdesc, s_piece, s_npc);
+    if (t_begin + 1 < t_end) load_pairs(t_begin + 1);
+    __syncthreads();
 
     const int lgw = LGW_T > 0 ? LGW_T : a.LGW;   // lanes per grad_output row (power of two)
     const int LG = RB / lgw;                  // lane groups (runs of pieces) per workgroup
@@ -532,25 +525,6 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
         if constexpr (kRelu) mrs = make_rsrc(a.mask + row0 * MW, static_cast<uint32_t>(ns) * F * MW * 4);
         if constexpr (kLin) xrs = make_rsrc(a.x + row0, static_cast<uint32_t>(ns) * F * 4);
     };
-    // the prefetched sub-tile's descriptors, pieces and piece count from the
-    // prefetch registers into LDS buffer b
-    auto stash = [&](int b) __attribute__((always_inline)) {
-        uint2 *dd = s_sdesc + b * (kP + 1);
-        uint32_t *ps = s_piece + b * PM;
-        reinterpret_cast<uint4 *>(dd)[tid] = pd0;
-        if constexpr (kDescRegs > 1) reinterpret_cast<uint4 *>(dd)[tid + RB] = pd1;
-        if (tid < PM) ps[tid] = pp0;
-        if (tid + RB < PM) ps[tid + RB] = pp1;
-        if (tid + 2 * RB < PM) ps[tid + 2 * RB] = pp2;
-        if constexpr (kPieceRegsRB > 3) {
-            if (tid + 3 * RB < PM) ps[tid + 3 * RB] = pp3;
-        }
-        if constexpr (kPieceRegsRB > 4) {
-            if (tid + 4 * RB < PM) ps[tid + 4 * RB] = pp4;
-        }
-        if (tid == 0) s_npc[b] = pnpc;
-    };
-
     // Piece tt of the current sub-tile's run: its entry, its rows'
     // descriptors, and loads of their gradient rows.  Past j1 the piece is
     // empty (all rows read zeros).  Every lane loads, with no branch around the load,
@@ -693,30 +667,41 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
         }
     };
 
-    // Two register buffers: piece tt+1 is in flight while piece tt is
-    // reduced.  m is the same for every run, so the loop is uniform; a piece
-    // issued past a run's end is empty.  A sub-tile's first piece is issued
-    // as soon as its descriptors are in LDS: with two LDS buffers (dbuf)
-    // before the previous sub-tile's dx stores and record merge, with one
-    // after them.
-    float gA[kL][VEC], gB[kL][VEC];
-    uint2 dA[kL], dB[kL];
-    uint32_t pA = 0, pB = 0;
-    uint32_t mA[kL], mB[kL];     // (epilogue with ReLU)
-    float xA[kL], xB[kL];        // (epilogue with linear0)
-    const bool dbuf = a.dbuf != 0;
-    auto begin_tile = [&](int t, int b) __attribute__((always_inline)) {
-        // (past the chunk's last sub-tile: the last one again, unused)
-        PLE_PREFETCH(t + 1 < t_end ? t + 1 : t);
-        set_tile(t, b);
-        if (m > 0) issue(0, gA, dA, pA, mA, xA);
+    // Three register buffers: pieces tt+1 and tt+2 are in flight while piece
+    // tt is reduced (enough bytes in flight for one workgroup to keep its
+    // CU's share of HBM busy while the other one sorts).  m is the same for
+    // every run, so the loop is uniform; a piece issued past a run's end is
+    // empty.  A sub-tile's first two pieces are issued as soon as its
+    // descriptors are in place.
+    float gA[kL][VEC], gB[kL][VEC], gC[kL][VEC];
+    uint2 dA[kL], dB[kL], dC[kL];
+    uint32_t pA = 0, pB = 0, pC = 0;
+    uint32_t mA[kL], mB[kL], mC[kL];     // (epilogue with ReLU)
+    float xA[kL], xB[kL], xC[kL];        // (epilogue with linear0)
+    auto begin_tile = [&](int t) __attribute__((always_inline)) {
+        set_tile(t, 0);
+        if (m > 0) {
+            issue(0, gA, dA, pA, mA, xA);
+            issue(1, gB, dB, pB, mB, xB);
+        }
     };
 
-    stash(0);
-    __syncthreads();
-    begin_tile(t_begin, 0);
+
+    // Per sub-tile t (its first piece in flight): the ranking part of sub-tile
+    // t + 1's sort (count buffer (t + 1 - t_begin) & 1; the other one is
+    // cleared for sub-tile t + 2), then F reduces t's pieces; after a barrier
+    // H and G store its dx and merge its run records, and the placing part
+    // of the sort fills the descriptor buffer for t + 1; after another
+    // barrier its first piece is issued.
+    begin_tile(t_begin);
     for (int t = t_begin; t < t_end; ++t) {
-        const int b = dbuf ? (t - t_begin) & 1 : 0;
+        const int bsel = (t - t_begin) & 1;       // count buffer of sub-tile t's sort
+        const bool more = t + 1 < t_end;
+        if (more) {
+            tile_rank<Q, RB>(a, t + 1, nfh, tid, pk, pv, s_nb, s_edge, s_iw, s_cnt + (bsel ^ 1) * cnt_half, ko, qb);
+            if (t + 2 < t_end) load_pairs(t + 2);
+        }
+        clear_counts(bsel);
 
         // F. pieces: lane group lg takes the contiguous pieces [j0, j1) (its
         //    "run"); piece 0 is in flight already
@@ -732,24 +717,22 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
         if (m > 0) {
             int tt = 0;
 #pragma unroll 1
-            for (; tt + 1 < m; tt += 2) {
-                issue(tt + 1, gB, dB, pB, mB, xB);
+            for (; tt + 2 < m; tt += 3) {
+                issue(tt + 2, gC, dC, pC, mC, xC);
                 process(tt, gA, dA, pA, mA, xA);
-                issue(tt + 2, gA, dA, pA, mA, xA);   // (unconditional: one block per step schedules better)
+                issue(tt + 3, gA, dA, pA, mA, xA);   // (unconditional: one block per step schedules better)
                 process(tt + 1, gB, dB, pB, mB, xB);
+                issue(tt + 4, gB, dB, pB, mB, xB);
+                process(tt + 2, gC, dC, pC, mC, xC);
             }
             if (tt < m) process(tt, gA, dA, pA, mA, xA);
+            if (tt + 1 < m) process(tt + 1, gB, dB, pB, mB, xB);
         }
         flush_key();
         if constexpr (kRawDb) flush_fl();
-        // the next sub-tile into the other buffer (its contents, two
-        // sub-tiles back, were last read before the previous barrier)
-        const bool more = t + 1 < t_end;
-        if (dbuf && more) stash(b ^ 1);
         __syncthreads();
         const int64_t h_sub = sub;
         const int h_ns = ns;
-        if (dbuf && more) begin_tile(t + 1, b ^ 1);
 
         // H. dx of the sub-tile, feature-major: coalesced stores
         if (a.dxt) {
@@ -804,32 +787,35 @@ __global__ __launch_bounds__(RB) void ple_bwd_reduce_kernel(BwdArgs a) {
                 }
             }
         }
-        // (with one buffer, F is over everywhere: its descriptors can go)
-        if (!dbuf && more) stash(0);
+        // S. the placing part of the next sub-tile's sort (its first barrier
+        //    also orders the record reads above before the next sub-tile's
+        //    record writes)
+        if (more) tile_place<RB>(a, tid, ko, qb, s_cnt + (bsel ^ 1) * cnt_half, s_seg, s_tmp, s_sdesc, s_piece, s_npc);
         // this barrier orders the dx reads before the next sub-tile's s_dx
-        // writes, and the histogram updates before its pieces
+        // writes, the histogram updates before its pieces, and the sort's
+        // descriptors before they are read
         __syncthreads();
-        if (!dbuf && more) begin_tile(t + 1, 0);
+        if (more) begin_tile(t + 1);
     }
-#undef PLE_PREFETCH
     __syncthreads();
 
     // chunk partials
     if (a.part) {
+        const int D2 = 2 * D;
         float *dst = a.part + (static_cast<int64_t>(c) * F + f0) * B * D2;
-        for (int i = tid; i < FS * B * D2; i += RB) {
+        for (int i = tid; i < FS * B * D2; i += NTH) {
             const int fl = i / (B * D2);
             const int k = (i - fl * B * D2) / D2;
             if (fl < nfh && k < s_nb[fl]) dst[i] = s_hist[i];
         }
         if constexpr (kRawDb) {
             float *dstb = a.part_db + (static_cast<int64_t>(c) * F + f0) * D;
-            for (int i = tid; i < FS * D; i += RB)
+            for (int i = tid; i < FS * D; i += NTH)
                 if (i / D < nfh) dstb[i] = s_db[i];
         }
         if constexpr (kLin) {
             float *dstl = a.part_lw + (static_cast<int64_t>(c) * F + f0) * D;
-            for (int i = tid; i < FS * D; i += RB)
+            for (int i = tid; i < FS * D; i += NTH)
                 if (i / D < nfh) dstl[i] = s_dlw[i];
         }
     }
@@ -1164,13 +1150,12 @@ struct BwdPlan {
     int rb;          // reduce workgroup size
     int C, Cd;
     int64_t NC;
-    size_t lds, sort_lds;
-    size_t part_bytes, part_db_bytes, part_lw_bytes, desc_bytes, piece_bytes, npc_bytes, dxt_bytes;
+    size_t lds;
+    size_t part_bytes, part_db_bytes, part_lw_bytes, dxt_bytes;
     BwdArgs geo;     // sorted-path geometry and LDS offsets
     size_t total() const {
         return align_up(part_bytes, 256) + align_up(part_db_bytes, 256) + align_up(part_lw_bytes, 256) +
-               align_up(desc_bytes, 256) +
-               align_up(piece_bytes, 256) + align_up(npc_bytes, 256) + align_up(dxt_bytes, 256);
+               align_up(dxt_bytes, 256);
     }
 };
 
@@ -1182,25 +1167,11 @@ struct LdsTaker {
     }
 };
 
-size_t sort_layout(BwdArgs &g, int FS, int B, int PM) {
-    LdsTaker take;
-    const size_t KB = static_cast<size_t>(B) + 1;
-    take(g.so_nb, 4ull * FS);
-    take(g.so_edge, 4ull * FS * KB);
-    take(g.so_iw, 4ull * FS * B);
-    take(g.so_cnt, 2ull * (kP / kWave) * FS * KB);
-    take(g.so_seg, 4ull * (FS * KB + 1));
-    take(g.so_tmp, 4ull * kWavesPerBlock);
-    take(g.so_desc, 8ull * kP);
-    take(g.so_piece, 4ull * PM);
-    return take.off;
-}
-
 // raw_db: records carry the raw-gradient bias sums too (quantised gradients,
-// linear0 epilogue); lin: and the linear0 weight sums
-// bufs: LDS buffers for the sub-tile descriptors, pieces and piece count
-// (two: the next sub-tile is staged while the current one is reduced)
-size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_db, bool lin, int bufs = 1) {
+// linear0 epilogue); lin: and the linear0 weight sums.  The sort's edges,
+// block counts, key starts and wave totals.
+size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_db, bool lin) {
+    constexpr int bufs = 1;
     LdsTaker take;
     take(g.ro_qw, 4ull * FS * B * D);
     take(g.ro_hist, 8ull * FS * B * D);
@@ -1216,6 +1187,10 @@ size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_
     take(g.ro_dx, 4ull * (kP + 1));
     take(g.ro_lw, lin ? 4ull * FS * D : 0ull);
     take(g.ro_dlw, lin ? 4ull * FS * D : 0ull);
+    take(g.ro_edge, 4ull * FS * (B + 1));
+    take(g.ro_cnt, 2ull * 2 * (kBlocks * FS * B + 1));
+    take(g.ro_seg, 4ull * (FS * B + 1));
+    take(g.ro_tmp, 4ull * (kWideBlock / kWave));
     return take.off;
 }
 
@@ -1228,17 +1203,15 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
     // Sorted path: bins fit the 12-bit field of a piece, and a sub-tile's
     // gradient rows span less than 2^31 bytes (32-bit buffer offsets).
     if (B <= 4096 && static_cast<int64_t>(kP) * F * D * 4 < INT32_MAX && tuning(PLE_TUNE_BWD_SIMPLE) == 0) {
-        // 4 floats per lane (16-byte loads for fp32 gradients) when D allows:
-        // 8 per lane halves the per-row instructions but needs registers for
-        // two waves per SIMD only, which hides less latency; lane groups of a
+        // 4 floats per lane (16-byte loads for fp32 gradients) when D allows
+        // (8 a lane halved the per-row instructions but needed registers for
+        // two waves per SIMD only, and hid less latency); lane groups of a
         // power-of-two width
         int vec = !g_align16 ? 1 : (D % 4 == 0 ? 4 : 1);
         // even D not a multiple of 4 (up to 64 columns): 2 floats per lane,
         // half the loads of one per lane and lane groups with DPP sums
         if (vec == 1 && g_align16 && D % 2 == 0 && D >= 6 && D <= 64) vec = 2;
-        const int vec_env = tuning(PLE_TUNE_BWD_VEC);    // 8 or 1 instead of the default
-        if (vec_env == 8 && D % 8 == 0 && g_align16 && !lin) vec = 8;
-        if (vec_env == 1) vec = 1;
+        if (tuning(PLE_TUNE_BWD_VEC) == 1) vec = 1;
         const int uv = static_cast<int>(D / vec);
         int lgw = 2;
         while (lgw < uv) lgw *= 2;
@@ -1249,7 +1222,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
             BwdArgs geo{};
             auto pm_for = [&](int fs) { return kP / kL + static_cast<int>(std::min<int64_t>(kP, fs * B)); };
             for (int fs = 4; fs >= 1; fs /= 2) {
-                if (fs > 1 && fs > F) continue;
+                if ((fs > 1 && fs > F) || static_cast<int64_t>(fs) * B >= 65536) continue;
                 BwdArgs t{};
                 const size_t lds = reduce_layout(t, fs, static_cast<int>(B), static_cast<int>(D), LG, pm_for(fs), raw_db, lin);
                 if (lds <= kReduceLdsTarget || (fs == 1 && lds <= kLdsMax)) {
@@ -1260,7 +1233,8 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                 }
             }
             const int fs_env = tuning(PLE_TUNE_BWD_FS);
-            if (fs_env == 1 || fs_env == 2 || fs_env == 4 || fs_env == 8 || fs_env == 16) {
+            if ((fs_env == 1 || fs_env == 2 || fs_env == 4 || fs_env == 8 || fs_env == 16) &&
+                static_cast<int64_t>(fs_env) * B < 65536) {
                 BwdArgs t{};
                 const size_t lds = reduce_layout(t, fs_env, static_cast<int>(B), static_cast<int>(D), LG, pm_for(fs_env), raw_db, lin);
                 if (lds <= kLdsMax) {
@@ -1269,7 +1243,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                     geo = t;
                 }
             }
-            int rb = kBlock, LGc = LG;
+            int rb = kBlock;
             if (best_fs > 0) {
                 const int PM = pm_for(best_fs);
                 // Twice the workgroup size where LDS leaves room for one
@@ -1277,7 +1251,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                 // linear0 branch): c2 -20 us; where two fit, the wide form
                 // measured slower (c3 +28 us, c4 +190 us).
                 {
-                    const bool wide_ok = !raw_db && vec != 8;
+                    const bool wide_ok = !raw_db;
                     bool wide = wide_ok && kLdsMax / best_lds < 2;
                     const int rb_env = tuning(PLE_TUNE_BWD_RB);
                     if (rb_env == kBlock || rb_env == kWideBlock) wide = wide_ok && rb_env == kWideBlock;
@@ -1289,42 +1263,20 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                             geo = tw;
                             best_lds = ldsw;
                             rb = kWideBlock;
-                            LGc = kWideBlock / lgw;
                         }
                     }
                 }
-                // Two descriptor buffers when two workgroups still fit a CU
-                // with them (c1: -7 us; where they would cost a resident
-                // workgroup, as at c3, they cost more than they save, and at
-                // one workgroup per CU, as at c2, they did not pay either).
                 {
-                    BwdArgs t2 = geo;
-                    const size_t lds2 = reduce_layout(t2, best_fs, static_cast<int>(B), static_cast<int>(D), LGc, PM,
-                                                      raw_db, lin, 2);
-                    const int dbuf_k = tuning(PLE_TUNE_BWD_DBUF);   // 1: one buffer, 2: two
-                    const bool dbuf = dbuf_k != 0 ? (dbuf_k == 2 && lds2 <= kLdsMax) : (kLdsMax / lds2 >= 2);
-                    if (dbuf) {
-                        geo = t2;
-                        best_lds = lds2;
-                    }
-                    geo.dbuf = dbuf ? 1 : 0;
-                }
-                const size_t slds = sort_layout(geo, best_fs, static_cast<int>(B), PM);
-                if (slds <= kLdsMax) {
                     pl.sorted = true;
                     pl.vec = vec;
                     pl.rb = rb;
                     pl.lds = best_lds;
-                    pl.sort_lds = slds;
                     geo.FS = best_fs;
                     geo.G = static_cast<int>((F + best_fs - 1) / best_fs);
                     geo.NT = kP / best_fs;
                     geo.T = static_cast<int>((N + geo.NT - 1) / geo.NT);
                     geo.PM = PM;
                     geo.LGW = lgw;
-                    int nbits = 0;
-                    while ((1ll << nbits) <= B) ++nbits;      // keys 0..B
-                    geo.nbits = nbits;
                     // chunks of sub-tiles: about PLE_TUNE_BWD_WG_PER_CU reduce
                     // workgroups per CU, within the partials budget.  Two per
                     // CU measured best at c1-c3 (4 per CU: +15 to +40 us, the
@@ -1340,10 +1292,6 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                     pl.C = pl.Cd = (geo.T + geo.SPC - 1) / geo.SPC;
                     pl.NC = static_cast<int64_t>(geo.SPC) * geo.NT;
                     pl.geo = geo;
-                    const int64_t tiles = static_cast<int64_t>(geo.T) * geo.G;
-                    pl.desc_bytes = static_cast<size_t>(tiles) * kP * sizeof(uint2);
-                    pl.piece_bytes = static_cast<size_t>(tiles) * PM * sizeof(uint32_t);
-                    pl.npc_bytes = static_cast<size_t>(tiles) * sizeof(int);
                     pl.dxt_bytes = static_cast<size_t>(N) * F * sizeof(float);
                 }
             }
@@ -1401,44 +1349,36 @@ const BwdPlan &plan_cached(int64_t N, int64_t F, int64_t B, int64_t D, bool g_al
     return e.pl;
 }
 
-// Bin indices are uint8 (up to 256 bins) or int16 (the sorted path takes at
-// most 4096 bins).
-template <int Q>
-hipError_t launch_sort(const BwdArgs &a, int idxb, dim3 grid, size_t lds, hipStream_t s) {
-    if (idxb == 1) hipLaunchKernelGGL((ple_bwd_sort_kernel<Q, uint8_t>), grid, dim3(kBlock), lds, s, a);
-    else hipLaunchKernelGGL((ple_bwd_sort_kernel<Q, int16_t>), grid, dim3(kBlock), lds, s, a);
-    return hipGetLastError();
-}
-
 // Lane-group width as a template argument (DPP reductions) for the 4- and
 // 2-float rows and the common one-column-a-lane widths; the other widths of
 // one column a lane take it at run time.
 template <int GD, int Q, int EPI, int RB>
 hipError_t launch_reduce_epi(const BwdArgs &a, int vec, dim3 grid, size_t lds, hipStream_t s) {
+    const dim3 blk(RB);
     if (vec == 4) {
         switch (a.LGW) {
-            case 2: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 2, EPI, RB>), grid, dim3(RB), lds, s, a); break;
-            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 4, EPI, RB>), grid, dim3(RB), lds, s, a); break;
-            case 8: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 8, EPI, RB>), grid, dim3(RB), lds, s, a); break;
-            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 4, 16, EPI, RB>), grid, dim3(RB), lds, s, a); break;
+            case 2: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 4, 2, EPI, RB>), grid, blk, lds, s, a); break;
+            case 4: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 4, 4, EPI, RB>), grid, blk, lds, s, a); break;
+            case 8: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 4, 8, EPI, RB>), grid, blk, lds, s, a); break;
+            default: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 4, 16, EPI, RB>), grid, blk, lds, s, a); break;
         }
     } else if (vec == 2) {
         // (the planner takes 2 per lane for 6 <= D <= 64: groups of 4 to 32 lanes)
         switch (a.LGW) {
-            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 2, 4, EPI, RB>), grid, dim3(RB), lds, s, a); break;
-            case 8: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 2, 8, EPI, RB>), grid, dim3(RB), lds, s, a); break;
-            case 16: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 2, 16, EPI, RB>), grid, dim3(RB), lds, s, a); break;
-            case 32: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 2, 32, EPI, RB>), grid, dim3(RB), lds, s, a); break;
+            case 4: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 2, 4, EPI, RB>), grid, blk, lds, s, a); break;
+            case 8: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 2, 8, EPI, RB>), grid, blk, lds, s, a); break;
+            case 16: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 2, 16, EPI, RB>), grid, blk, lds, s, a); break;
+            case 32: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 2, 32, EPI, RB>), grid, blk, lds, s, a); break;
             default: return hipErrorInvalidConfiguration;
         }
     } else {
         // one column a lane: DPP group sums for the 16- to 64-lane groups
         // (9 <= D <= 64), shuffles at run time for the others
         switch (a.LGW) {
-            case 16: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 16, EPI, RB>), grid, dim3(RB), lds, s, a); break;
-            case 32: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 32, EPI, RB>), grid, dim3(RB), lds, s, a); break;
-            case 64: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 64, EPI, RB>), grid, dim3(RB), lds, s, a); break;
-            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 1, 0, EPI, RB>), grid, dim3(RB), lds, s, a); break;
+            case 16: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 1, 16, EPI, RB>), grid, blk, lds, s, a); break;
+            case 32: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 1, 32, EPI, RB>), grid, blk, lds, s, a); break;
+            case 64: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 1, 64, EPI, RB>), grid, blk, lds, s, a); break;
+            default: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 1, 0, EPI, RB>), grid, blk, lds, s, a); break;
         }
     }
     return hipGetLastError();
@@ -1450,27 +1390,20 @@ template <int GD, int Q>
 hipError_t launch_reduce(const BwdArgs &a, int vec, int epi, int rb, dim3 grid, size_t lds, hipStream_t s) {
     if (rb == kWideBlock) {
         if constexpr (GD == PLE_DTYPE_F32 && Q == PLE_DTYPE_F32) {
-            if (vec != 8 && epi == 0) return launch_reduce_epi<GD, Q, 0, kWideBlock>(a, vec, grid, lds, s);
-            if (vec != 8 && epi == kBwdRelu) return launch_reduce_epi<GD, Q, kBwdRelu, kWideBlock>(a, vec, grid, lds, s);
+            if (epi == 0) return launch_reduce_epi<GD, Q, 0, kWideBlock>(a, vec, grid, lds, s);
+            if (epi == kBwdRelu) return launch_reduce_epi<GD, Q, kBwdRelu, kWideBlock>(a, vec, grid, lds, s);
         }
         return hipErrorInvalidConfiguration;   // (the planner never asks for it elsewhere)
     }
     if constexpr (GD == PLE_DTYPE_F32) {
-        // module epilogues (their gradient is fp32); no 8-float rows
+        // module epilogues (their gradient is fp32)
         switch (epi) {
             case kBwdRelu: return launch_reduce_epi<GD, Q, kBwdRelu, kBlock>(a, vec, grid, lds, s);
             case kBwdLin: return launch_reduce_epi<GD, Q, kBwdLin, kBlock>(a, vec, grid, lds, s);
-            case kBwdLin | kBwdRelu: return launch_reduce_epi<GD, Q, kBwdLin | kBwdRelu, kBlock>(a, vec, grid, lds, s);
+            case kBwdLin | kBwdRelu:
+                return launch_reduce_epi<GD, Q, kBwdLin | kBwdRelu, kBlock>(a, vec, grid, lds, s);
             default: break;
         }
-    }
-    if (vec == 8) {
-        switch (a.LGW) {
-            case 2: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 2, 0, kBlock>), grid, dim3(kBlock), lds, s, a); break;
-            case 4: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 4, 0, kBlock>), grid, dim3(kBlock), lds, s, a); break;
-            default: hipLaunchKernelGGL((ple_bwd_reduce_kernel<GD, Q, 8, 8, 0, kBlock>), grid, dim3(kBlock), lds, s, a); break;
-        }
-        return hipGetLastError();
     }
     return launch_reduce_epi<GD, Q, 0, kBlock>(a, vec, grid, lds, s);
 }
@@ -1481,10 +1414,9 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
     const int epi = (a.mask ? kBwdRelu : 0) | (a.lin_w ? kBwdLin : 0);
     if (pl.sorted) {
         a.db_from_buckets = Q == PLE_DTYPE_F32 && a.lin_w == nullptr;
-        e = launch_sort<Q>(a, idxb, dim3(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, a.T))), pl.sort_lds, s);
-        if (e != hipSuccess) return e;
-        e = launch_reduce<GD, Q>(a, pl.vec, epi, pl.rb, dim3(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, pl.C))),
-                                 pl.lds, s);
+        const dim3 grid(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, pl.C)));
+        a.idxb = idxb;
+        e = launch_reduce<GD, Q>(a, pl.vec, epi, pl.rb, grid, pl.lds, s);
         if (e != hipSuccess) return e;
         if (a.dxt) {
             const dim3 tg(static_cast<unsigned>((a.N + kTr - 1) / kTr), static_cast<unsigned>((a.F + kTr - 1) / kTr));
@@ -1611,8 +1543,7 @@ int backward_run(const BackwardRequest &r) {
     if (need > 0 && (r.workspace == nullptr || r.workspace_bytes < need ||
                      reinterpret_cast<uintptr_t>(r.workspace) % 256 != 0))
         return PLE_E_WORKSPACE;
-    const int64_t grid_max = pl.sorted ? kNumXcd * std::max(tiles_per_xcd(pl.geo.G, pl.geo.T), tiles_per_xcd(pl.geo.G, pl.C))
-                                       : static_cast<int64_t>(r.F) * pl.C;
+    const int64_t grid_max = pl.sorted ? kNumXcd * tiles_per_xcd(pl.geo.G, pl.C) : static_cast<int64_t>(r.F) * pl.C;
     if (grid_max > INT32_MAX) return PLE_E_TOO_LARGE;
     BwdArgs a = pl.geo;
     a.g = r.g; a.x = r.x; a.edges = r.edges; a.iw = r.iw; a.nbins = r.nbins; a.weight = r.weight;
@@ -1633,9 +1564,6 @@ int backward_run(const BackwardRequest &r) {
     a.part_db = want_dwdb ? part_db : nullptr;
     a.part_lw = want_dwdb && lin ? part_lw : nullptr;
     if (pl.sorted) {
-        a.desc = reinterpret_cast<uint2 *>(carve(pl.desc_bytes));
-        a.piece = reinterpret_cast<uint32_t *>(carve(pl.piece_bytes));
-        a.npc = reinterpret_cast<int *>(carve(pl.npc_bytes));
         float *dxt = reinterpret_cast<float *>(carve(pl.dxt_bytes));
         a.dxt = want_dx ? dxt : nullptr;
     }

@@ -348,27 +348,6 @@ def test_two_column_lanes_match_one_column_lanes(d, c_oracle, tune):
     _check_backward(w, "f32", g, gx, gw, gb, c_oracle)
 
 
-@pytest.mark.parametrize("cfg", [1, 3])
-def test_backward_descriptor_buffering_modes_agree(cfg, c_oracle, tune):
-    """One or two LDS buffers for the sorted descriptors (the planner picks by
-    LDS room; the BWD_DBUF knob forces either): same pieces, same order of every
-    sum, so bitwise the same gradients, both checked against the oracle."""
-    w = workloads.make(cfg, REDUCED[cfg])
-    n, f, bmax, d = w.shape
-    print(f"buffering modes {w.name} shape={w.shape}", flush=True)
-    x, e, iw, nb, wt, bt = _inputs(w)
-    _, idx = ops.forward_with_bias(x, e, iw, nb, wt, bt, torch.float32)
-    g = _grad((n, f, d), 11)
-    res = []
-    for mode in (1, 2):
-        tune("BWD_DBUF", mode)
-        res.append(ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, True, True, True))
-    tune("BWD_DBUF", 0)
-    for a_, b_ in zip(*res):
-        assert torch.equal(a_, b_)
-    _check_backward(w, "f32", g, *res[1], c_oracle)
-
-
 @pytest.mark.parametrize("cfg", [0, 1, 2, 3])
 def test_fallback_backward_path_matches_oracle(cfg, c_oracle, tune):
     """The simple (non-fused) backward kernels, forced by the BWD_SIMPLE knob."""
