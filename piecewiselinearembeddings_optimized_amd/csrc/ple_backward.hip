@@ -16,30 +16,29 @@
 //
 // Main path: ple_bwd_fused_kernel, over tiles of P (sample, feature) pairs
 // (NT samples x FS features, "sub-tiles").  One workgroup per feature group
-// and chunk of SPC sub-tiles: four (or eight) reducer waves and one sorter
-// wave, which sorts sub-tile t + 1 into one LDS buffer while the reducers
-// reduce sub-tile t from the other.
+// and chunk of SPC sub-tiles; every thread takes part in both jobs, which
+// interleave sub-tile by sub-tile:
 //
-// sorter -- reads the bin index and x of every pair, computes q(frac) and the
-//   edge flag, and counting-sorts the pairs by (feature, bin): per 64-pair
-//   block, ranks of equal keys from 64-bit ballots plus the key's running
-//   count, then a wave scan over the keys -- deterministic and stable.
-//   Writes the sorted row descriptors {q(frac) (-0 marks x on the bin's left
-//   edge), sample | feature << 24} and the sub-tile's pieces: every (feature,
-//   bin) run of sorted rows cut into pieces of kL rows.  Nothing leaves LDS.
+// sort -- the bin index and x of every pair of the next sub-tile (loaded a
+//   sub-tile ahead) give q(frac) and the edge flag; a counting sort by
+//   (feature, bin): per 64-pair block, ranks of equal keys from 64-bit
+//   ballots plus the key's count in the block, then a scan over the keys --
+//   deterministic and stable.  It writes the sorted row descriptors
+//   {q(frac) (-0 marks x on the bin's left edge), sample | feature << 24} and
+//   the sub-tile's pieces: every (feature, bin) run of sorted rows cut into
+//   pieces of kL rows.  Nothing leaves LDS.
 //
-// reducers -- nothing but the gradient stream and LDS work.  Lane groups
-//   (D/VEC lanes, one grad_output row per step) take equal runs of pieces:
-//   each row is read once, its dx is the lane group's DPP-reduced dot with
-//   the LDS weight row (kept in LDS at its sorted position), and bucket /
+// reduce -- the gradient stream and LDS work.  Lane groups (D/VEC lanes, one
+//   grad_output row per step) take equal runs of pieces: each row is read
+//   once, its dx is the lane group's DPP-reduced dot with the LDS weight row
+//   (kept in the row's descriptor once the row is reduced), and bucket /
 //   weighted / bias sums run in registers until the key changes (checked
 //   once per piece).  A run's first key goes to a per-run record, every later
 //   key straight into the LDS histogram (no other run can own it); the
-//   records are added run by run in order.  Each row's dx is staged in LDS
-//   at its pair's position (the descriptor names it) and leaves
-//   feature-major in whole lines.  The chunk's histogram is written once.
+//   records are added run by run in order.  The sub-tile's dx leaves from
+//   the descriptors straight into dx [N, F].  The chunk's histogram is
+//   written once.
 //
-// ple_bwd_dx_transpose_kernel turns the feature-major dx into [N, F];
 // ple_bwd_chunksum_kernel adds the chunk partials in chunk order;
 // ple_bwd_finalize_kernel takes the suffix over bins.
 //
@@ -72,7 +71,6 @@ struct BwdArgs {
     float *db;
     float *part;     // [Cd][F][B][2D] chunk partials {bucket | weighted}
     float *part_db;  // [Cd][F][D] chunk partials of the bias gradient
-    float *dxt;      // [F][N] dx, feature-major (transposed into dx at the end)
     const uint32_t *mask;   // [N][F][MW] ReLU pass bits of the forward (epilogue with ReLU)
     const float *lin_w;     // [F][D] linear0 weight (version-B epilogue)
     float *part_lw;         // [Cd][F][D] chunk partials of the linear0 weight gradient
@@ -90,7 +88,7 @@ struct BwdArgs {
     // sorted path
     int FS, G, NT, T, SPC, PM, LGW;   // T sub-tiles, SPC sub-tiles per chunk, PM piece capacity
     int ro_qw, ro_hist, ro_db, ro_iw, ro_nb, ro_desc, ro_piece, ro_npc, ro_rec, ro_rkey, ro_rfl, ro_dx,
-        ro_lw, ro_dlw, ro_edge, ro_cnt, ro_seg, ro_tmp;   // fused kernel LDS
+        ro_lw, ro_dlw, ro_edge, ro_cnt, ro_seg, ro_tmp;   // fused kernel LDS (ro_dx < 0: no dx staging)
 };
 
 constexpr int kP = 1024;                        // (sample, feature) pairs per sub-tile
@@ -111,6 +109,9 @@ constexpr int kBwdLin = 2;
 // ---------------------------------------------------------------------------
 
 constexpr int kBlocks = kP / kWave;   // 64-pair blocks of a sub-tile
+
+// uint16 block counts per block row: NK keys, padded to whole dwords
+__host__ __device__ __forceinline__ int cnt_stride(int NK) { return (NK + 1) & ~1; }
 
 // Bin index and x of this thread's pairs of sub-tile t: pairs p = tid + u RB
 // in sample-major order (p = s * FS + fl), so a load instruction covers whole
@@ -141,8 +142,8 @@ __device__ __forceinline__ void tile_load(const BwdArgs &a, int t, int f0, int n
 //      keys of its 64-pair block (64-bit ballots over the bin bits within the
 //      lanes of its feature -- a lane's feature is the same in every block);
 //      the block's first pair of each key stores the key's count in the block
-//      (s_cnt, zero beforehand).  Per pair key | rank << 16 and the q(frac)
-//      bits stay in registers.
+//      (s_cnt, whose row the ranking wave zeroes first).  Per pair
+//      key | rank << 16 and the q(frac) bits stay in registers.
 //   B. per key (each thread a contiguous run of keys): the exclusive prefix
 //      of its block counts in place, then a scan over the keys gives every key
 //      its first row and first piece (pieces: the key's rows cut into runs of
@@ -153,7 +154,8 @@ __device__ __forceinline__ void tile_load(const BwdArgs &a, int t, int f0, int n
 //      (rows - 1) << 28} from each piece's first row.
 // Pairs outside the batch or feature range take key NK and are not stored.
 // The caller synchronises between the parts, before the descriptors are
-// read, and before s_cnt is cleared for a later sort.
+// read, and between this sort's part B / C and the next sort's part A (one
+// count buffer).
 template <int Q, int RB>
 __device__ __forceinline__ void tile_rank(const BwdArgs &a, int t, int nfh, int tid, const int (&pk)[kP / RB],
                                           const float (&pv)[kP / RB], const int *s_nb, const float *s_edge,
@@ -181,6 +183,15 @@ __device__ __forceinline__ void tile_rank(const BwdArgs &a, int t, int nfh, int 
     const float *erow = s_edge + fl * (B + 1);
     const float *irow = s_iw + fl * B;
     const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+    // Each block's count row belongs to the one wave that ranks the block:
+    // that wave zeroes the row first (its own stores stay in order, and the
+    // previous sort's reads of the row finished before the caller's barrier).
+    const int CS = cnt_stride(NK);
+#pragma unroll
+    for (int u = 0; u < kPR; ++u) {
+        uint32_t *row = reinterpret_cast<uint32_t *>(s_cnt + ((tid + u * RB) >> 6) * CS);
+        for (int i = lane; i < CS / 2; i += kWave) row[i] = 0u;
+    }
 
     // A. keys and ranks: key | rank << 16 (keys below 2^16, ranks below 64)
 #pragma unroll
@@ -204,7 +215,7 @@ __device__ __forceinline__ void tile_rank(const BwdArgs &a, int t, int nfh, int 
         }
         const int rank = __popcll(m & lt);
         const int key = valid ? fl * B + k : NK;
-        if (rank == 0 && key < NK) s_cnt[(p >> 6) * NK + key] = static_cast<uint16_t>(__popcll(m));
+        if (rank == 0 && key < NK) s_cnt[(p >> 6) * CS + key] = static_cast<uint16_t>(__popcll(m));
         ko[u] = key | (rank << 16);
     }
 }
@@ -220,6 +231,7 @@ __device__ __forceinline__ void tile_place(const BwdArgs &a, int tid, const int 
     const int lane = tid & (kWave - 1);
     const int wv = tid / kWave;
     const int fl = lane & (FS - 1);
+    const int CS = cnt_stride(NK);
 
     // B. per key: block prefixes in place, then the scan over keys (rows in
     //    the low half, pieces in the high half; both below 2^16)
@@ -231,11 +243,11 @@ __device__ __forceinline__ void tile_place(const BwdArgs &a, int tid, const int 
         uint16_t *col = s_cnt + j;
         int cc[kBlocks];
 #pragma unroll
-        for (int b = 0; b < kBlocks; ++b) cc[b] = col[b * NK];
+        for (int b = 0; b < kBlocks; ++b) cc[b] = col[b * CS];
         int run = 0;
 #pragma unroll
         for (int b = 0; b < kBlocks; ++b) {
-            col[b * NK] = static_cast<uint16_t>(run);
+            col[b * CS] = static_cast<uint16_t>(run);
             run += cc[b];
         }
         s_seg[j] = run;
@@ -276,7 +288,7 @@ __device__ __forceinline__ void tile_place(const BwdArgs &a, int tid, const int 
             const int p = tid + u * RB;
             const int s = p >> fs_shift;
             const int st = s_seg[key];
-            const int within = s_cnt[(p >> 6) * NK + key] + (ko[u] >> 16);
+            const int within = s_cnt[(p >> 6) * CS + key] + (ko[u] >> 16);
             const int slot = (st & 0xffff) + within;
             desc[slot] = make_uint2(qb[u], static_cast<uint32_t>(s) | (static_cast<uint32_t>(fl) << 24));
             if (within % kL == 0) {
@@ -311,17 +323,19 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
     float *s_db = reinterpret_cast<float *>(lds + a.ro_db);             // [FS][D]
     float *s_iw = reinterpret_cast<float *>(lds + a.ro_iw);             // [FS][B]
     int *s_nb = reinterpret_cast<int *>(lds + a.ro_nb);                 // [FS]
-    uint2 *s_sdesc = reinterpret_cast<uint2 *>(lds + a.ro_desc);        // [P+1]: sorted rows, then a dummy row
+    // [P+2]: sorted rows, a dummy row, a discard slot.  Once a row's piece
+    // is reduced, its dx replaces its q(frac) bits (.x), unless the dx are
+    // staged in pair order (several features a group).
+    uint2 *s_sdesc = reinterpret_cast<uint2 *>(lds + a.ro_desc);
     uint32_t *s_piece = reinterpret_cast<uint32_t *>(lds + a.ro_piece); // [PM]
     int *s_npc = reinterpret_cast<int *>(lds + a.ro_npc);               // [1]
     float *s_edge = reinterpret_cast<float *>(lds + a.ro_edge);         // [FS][B+1] (sort)
-    uint16_t *s_cnt = reinterpret_cast<uint16_t *>(lds + a.ro_cnt);     // [2][P/64][FS*B] block counts (sort)
+    uint16_t *s_cnt = reinterpret_cast<uint16_t *>(lds + a.ro_cnt);     // [P/64][cnt_stride(FS*B)] block counts (sort)
     int *s_seg = reinterpret_cast<int *>(lds + a.ro_seg);               // [FS*B+1] key starts (sort)
     int *s_tmp = reinterpret_cast<int *>(lds + a.ro_tmp);               // [RB/64] (sort)
     float *s_rec = reinterpret_cast<float *>(lds + a.ro_rec);           // [LG][RS]
     int *s_rkey = reinterpret_cast<int *>(lds + a.ro_rkey);             // [LG]
-    int *s_rfl = reinterpret_cast<int *>(lds + a.ro_rfl);               // [LG]
-    float *s_dx = reinterpret_cast<float *>(lds + a.ro_dx);             // [P+1] dx by pair, fl * NT + s (+ a discard slot)
+    int *s_rfl = reinterpret_cast<int *>(lds + a.ro_rfl);               // [LG] (kRawDb)
     float *s_lw = reinterpret_cast<float *>(lds + a.ro_lw);             // [FS][D] linear0 weight
     float *s_dlw = reinterpret_cast<float *>(lds + a.ro_dlw);           // [FS][D] sum of g x
 
@@ -344,14 +358,6 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
         else tile_load<RB, int16_t>(a, t, f0, nfh, tid, pk, pv);
     };
     load_pairs(t_begin);
-    // the sort's block counts start at zero: two buffers, one for the sort in
-    // progress, one cleared for the sort after it (dwords: two counts each)
-    const int NK = FS * B;
-    const int cnt_half = ((kBlocks * NK + 1) / 2) * 2;        // counts per buffer (even)
-    auto clear_counts = [&](int bsel) __attribute__((always_inline)) {
-        uint32_t *w = reinterpret_cast<uint32_t *>(s_cnt + bsel * cnt_half);
-        for (int i = tid; i < cnt_half / 2; i += NTH) w[i] = 0u;
-    };
     int ko[kP / RB];          // the next sub-tile's keys | ranks, and q(frac) bits
     uint32_t qb[kP / RB];
 
@@ -359,8 +365,6 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
     // Rows past a piece's end read the dummy row kP: q(frac) = +0 and sample
     // NT, whose gradient offset lies past every sub-tile's span (zeros).
     if (tid == 0) s_sdesc[kP] = make_uint2(0u, static_cast<uint32_t>(NT));
-    clear_counts(0);
-    clear_counts(1);
     for (int i = tid; i < FS; i += NTH) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
     for (int i = tid; i < FS * B; i += NTH) {
         const int fl = i / B;
@@ -408,11 +412,17 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
     const int D2 = 2 * D;
     // record stride {bucket | weighted (| raw g) (| g x)}
     const int RS = (kRawDb ? 3 * D : 2 * D) + (kLin ? D : 0);
-    const int nt_shift = __ffs(NT) - 1;           // NT is a power of two
-    // dx slot of a row: its pair's position (feature-major, fl * NT + s), so
-    // that the sub-tile's dx leaves in pair order
+    // dx of sorted row j: dword 2 j of the descriptors (row kP + 1 takes the
+    // rows past a piece's end)
+    uint32_t *s_dxw = reinterpret_cast<uint32_t *>(s_sdesc);
+    // With several features a group the dx go through a staging buffer in
+    // pair order (sample-major, s * FS + fl; slot kP discards) instead, so
+    // that a sample's features leave in one store.
+    const bool dx_staged = a.ro_dx >= 0;
+    float *s_dx = reinterpret_cast<float *>(lds + (dx_staged ? a.ro_dx : 0));
+    const int fs_shift = __ffs(FS) - 1;
     auto dx_slot = [&](uint32_t y) __attribute__((always_inline)) {
-        return static_cast<int>(((y >> 24) << nt_shift) + (y & 0xffffff));
+        return static_cast<int>(((y & 0xffffff) << fs_shift) + (y >> 24));
     };
 
     // F-phase state of a run: running sums of its current key (feature,
@@ -464,7 +474,7 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
                 lds_store_vec<VEC>(dx2, o);
             }
         }
-        if (first_fl && lc == 0) s_rfl[lg] = db_fl;
+        if (first_fl && lc == 0) s_rfl[lg] = db_fl;   // (kRawDb only)
         first_fl = false;
     };
 
@@ -639,8 +649,9 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
             // x on the bin's left edge (k >= 1): the lower bin's term too
             parts[i] = dsc[i].x == 0x80000000u ? fmaf(dot2, iwp, part) : part;
         }
-        // dx into LDS by sorted row (rows past the piece's end: the
+        // dx into the rows' descriptors (rows past the piece's end: the
         // discard slot)
+        const int rs = static_cast<int>((pe >> 16) & 0xfff);
         if constexpr (LGW_T >= 4) {
             // reduce-scatter: each lane ends with one row's sum (32- and
             // 64-lane groups: within each 16-lane row, then across the rows)
@@ -648,21 +659,26 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
             constexpr int kW = LGW_T >= 32 ? 16 : LGW_T;
             constexpr int kLog = kW == 4 ? 2 : (kW == 8 ? 3 : 4);
             const int r = (((lc >> (kLog - 1)) & 1) << 1) | ((lc >> (kLog - 2)) & 1);
-            // (selects on named values: indexing the descriptor array
-            // with r would put it in scratch memory)
-            const uint32_t y0 = dsc[0].y, y1 = dsc[1].y, y2 = dsc[2].y, y3 = dsc[3].y;
-            const uint32_t yr = (r & 2) ? ((r & 1) ? y3 : y2) : ((r & 1) ? y1 : y0);
             float v = group_reduce_scatter4<kW>(parts, lc & (kW - 1));
             if constexpr (LGW_T >= 32) v += __shfl_xor(v, 16);
             if constexpr (LGW_T == 64) v += __shfl_xor(v, 32);
-            s_dx[r < n ? dx_slot(yr) : kP] = v;
+            if (dx_staged) {
+                // (selects on named values: indexing the descriptor array
+                // with r would put it in scratch memory)
+                const uint32_t y0 = dsc[0].y, y1 = dsc[1].y, y2 = dsc[2].y, y3 = dsc[3].y;
+                const uint32_t yr = (r & 2) ? ((r & 1) ? y3 : y2) : ((r & 1) ? y1 : y0);
+                s_dx[r < n ? dx_slot(yr) : kP] = v;
+            } else {
+                s_dxw[2 * (r < n ? rs + r : kP + 1)] = __float_as_uint(v);
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < kL; ++i) {
                 float v = parts[i];
                 if constexpr (LGW_T > 0) v = group_sum<LGW_T>(v);
                 else v = group_sum_rt(v, lgw);
-                s_dx[i < n ? dx_slot(dsc[i].y) : kP] = v;
+                if (dx_staged) s_dx[i < n ? dx_slot(dsc[i].y) : kP] = v;
+                else s_dxw[2 * (i < n ? rs + i : kP + 1)] = __float_as_uint(v);
             }
         }
     };
@@ -687,21 +703,18 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
     };
 
 
-    // Per sub-tile t (its first piece in flight): the ranking part of sub-tile
-    // t + 1's sort (count buffer (t + 1 - t_begin) & 1; the other one is
-    // cleared for sub-tile t + 2), then F reduces t's pieces; after a barrier
-    // H and G store its dx and merge its run records, and the placing part
-    // of the sort fills the descriptor buffer for t + 1; after another
-    // barrier its first piece is issued.
+    // Per sub-tile t (its first pieces in flight): the ranking part of sub-tile
+    // t + 1's sort, then F reduces t's pieces; after a barrier H and G store
+    // its dx and merge its run records, and the placing part of the sort
+    // fills the descriptor buffer for t + 1; after another barrier its first
+    // pieces are issued.
     begin_tile(t_begin);
     for (int t = t_begin; t < t_end; ++t) {
-        const int bsel = (t - t_begin) & 1;       // count buffer of sub-tile t's sort
         const bool more = t + 1 < t_end;
         if (more) {
-            tile_rank<Q, RB>(a, t + 1, nfh, tid, pk, pv, s_nb, s_edge, s_iw, s_cnt + (bsel ^ 1) * cnt_half, ko, qb);
+            tile_rank<Q, RB>(a, t + 1, nfh, tid, pk, pv, s_nb, s_edge, s_iw, s_cnt, ko, qb);
             if (t + 2 < t_end) load_pairs(t + 2);
         }
-        clear_counts(bsel);
 
         // F. pieces: lane group lg takes the contiguous pieces [j0, j1) (its
         //    "run"); piece 0 is in flight already
@@ -712,7 +725,7 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
         for (int q = 0; q < VEC; ++q) ab[q] = aw[q] = ad[q] = ax[q] = 0.0f;
         if (lc == 0) {
             s_rkey[lg] = -1;
-            s_rfl[lg] = -1;
+            if constexpr (kRawDb) s_rfl[lg] = -1;
         }
         if (m > 0) {
             int tt = 0;
@@ -734,14 +747,27 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
         const int64_t h_sub = sub;
         const int h_ns = ns;
 
-        // H. dx of the sub-tile, feature-major: coalesced stores
-        if (a.dxt) {
+        // H. dx of the sub-tile's rows (one per valid pair: ns * nfh), from
+        //    the staging buffer or the descriptors straight into dx [N, F].
+        //    The lines of a sample's features fill up in the L2 of the XCD,
+        //    which runs every feature group of the chunk (decode_tile).
+        if (a.dx && dx_staged) {
 #pragma unroll
             for (int u = 0; u < (kP / RB); ++u) {
                 const int p = tid + u * RB;
-                const int fl = p >> nt_shift;
-                const int sidx = p & (NT - 1);
-                if (fl < nfh && sidx < h_ns) a.dxt[static_cast<int64_t>(f0 + fl) * a.N + h_sub + sidx] = s_dx[p];
+                const int sidx = p >> fs_shift;
+                const int fl = p & (FS - 1);
+                if (fl < nfh && sidx < h_ns) a.dx[(h_sub + sidx) * F + f0 + fl] = s_dx[p];
+            }
+        } else if (a.dx) {
+            const int rows = h_ns * nfh;
+#pragma unroll
+            for (int u = 0; u < (kP / RB); ++u) {
+                const int j = tid + u * RB;
+                if (j < rows) {
+                    const uint2 d = s_sdesc[j];
+                    a.dx[(h_sub + (d.y & 0xffffff)) * F + f0 + (d.y >> 24)] = __uint_as_float(d.x);
+                }
             }
         }
 
@@ -768,7 +794,7 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
                 }
             }
             const int rfl = kRawDb ? s_rfl[lg] : -1;
-            if (rfl >= 0 && (lg == 0 || s_rfl[lg - 1] != rfl)) {
+            if (kRawDb && rfl >= 0 && (lg == 0 || s_rfl[lg - 1] != rfl)) {
                 float sd[VEC], sx[VEC];
 #pragma unroll
                 for (int q = 0; q < VEC; ++q) sd[q] = sx[q] = 0.0f;
@@ -790,10 +816,10 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
         // S. the placing part of the next sub-tile's sort (its first barrier
         //    also orders the record reads above before the next sub-tile's
         //    record writes)
-        if (more) tile_place<RB>(a, tid, ko, qb, s_cnt + (bsel ^ 1) * cnt_half, s_seg, s_tmp, s_sdesc, s_piece, s_npc);
-        // this barrier orders the dx reads before the next sub-tile's s_dx
-        // writes, the histogram updates before its pieces, and the sort's
-        // descriptors before they are read
+        if (more) tile_place<RB>(a, tid, ko, qb, s_cnt, s_seg, s_tmp, s_sdesc, s_piece, s_npc);
+        // this barrier orders the histogram updates before the next
+        // sub-tile's pieces, the sort's descriptors before they are read, and
+        // the count reads before the next ranking zeroes them
         __syncthreads();
         if (more) begin_tile(t + 1);
     }
@@ -1086,55 +1112,6 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dx: feature-major [F][N] -> [N][F]
-// ---------------------------------------------------------------------------
-
-constexpr int kTr = 64;   // transpose tile (samples x features)
-
-// V4: 16-byte loads along samples and stores along features (N and F
-// multiples of 4); otherwise one element per access.
-template <bool V4>
-__global__ __launch_bounds__(kBlock) void ple_bwd_dx_transpose_kernel(const float *__restrict__ src, float *__restrict__ dst,
-                                                                   int64_t N, int F) {
-    __shared__ float tile[kTr][kTr + 1];   // [feature][sample]
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kTr;
-    const int f0 = blockIdx.y * kTr;
-    const int tid = threadIdx.x;
-    if constexpr (V4) {
-        const int c4 = tid % (kTr / 4);
-        for (int r = tid / (kTr / 4); r < kTr; r += kBlock / (kTr / 4)) {
-            const int f = f0 + r;
-            const int64_t n = n0 + 4 * c4;
-            if (f < F && n < N) {
-                const float4 v = *reinterpret_cast<const float4 *>(src + static_cast<int64_t>(f) * N + n);
-                tile[r][4 * c4] = v.x; tile[r][4 * c4 + 1] = v.y; tile[r][4 * c4 + 2] = v.z; tile[r][4 * c4 + 3] = v.w;
-            }
-        }
-        __syncthreads();
-        for (int r = tid / (kTr / 4); r < kTr; r += kBlock / (kTr / 4)) {
-            const int64_t n = n0 + r;
-            const int f = f0 + 4 * c4;
-            if (f < F && n < N)
-                *reinterpret_cast<float4 *>(dst + n * F + f) =
-                    make_float4(tile[4 * c4][r], tile[4 * c4 + 1][r], tile[4 * c4 + 2][r], tile[4 * c4 + 3][r]);
-        }
-    } else {
-        const int tx = tid % kTr;
-        for (int r = tid / kTr; r < kTr; r += kBlock / kTr) {
-            const int f = f0 + r;
-            const int64_t n = n0 + tx;
-            if (f < F && n < N) tile[r][tx] = src[static_cast<int64_t>(f) * N + n];
-        }
-        __syncthreads();
-        for (int r = tid / kTr; r < kTr; r += kBlock / kTr) {
-            const int64_t n = n0 + r;
-            const int f = f0 + tx;
-            if (f < F && n < N) dst[n * F + f] = tile[tx][r];
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
 // planning
 // ---------------------------------------------------------------------------
 
@@ -1151,11 +1128,10 @@ struct BwdPlan {
     int C, Cd;
     int64_t NC;
     size_t lds;
-    size_t part_bytes, part_db_bytes, part_lw_bytes, dxt_bytes;
+    size_t part_bytes, part_db_bytes, part_lw_bytes;
     BwdArgs geo;     // sorted-path geometry and LDS offsets
     size_t total() const {
-        return align_up(part_bytes, 256) + align_up(part_db_bytes, 256) + align_up(part_lw_bytes, 256) +
-               align_up(dxt_bytes, 256);
+        return align_up(part_bytes, 256) + align_up(part_db_bytes, 256) + align_up(part_lw_bytes, 256);
     }
 };
 
@@ -1172,25 +1148,27 @@ struct LdsTaker {
 // block counts, key starts and wave totals.
 size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_db, bool lin) {
     constexpr int bufs = 1;
+    const int NK = FS * B;
     LdsTaker take;
     take(g.ro_qw, 4ull * FS * B * D);
     take(g.ro_hist, 8ull * FS * B * D);
     take(g.ro_db, 4ull * FS * D);
     take(g.ro_iw, 4ull * FS * B);
     take(g.ro_nb, 4ull * FS);
-    take(g.ro_desc, bufs * 8ull * (kP + 1));
+    take(g.ro_desc, bufs * 8ull * (kP + 2));
     take(g.ro_piece, bufs * 4ull * PM);
     take(g.ro_npc, bufs * 4ull);
     take(g.ro_rec, (8ull + (raw_db ? 4ull : 0ull) + (lin ? 4ull : 0ull)) * LG * D);
     take(g.ro_rkey, 4ull * LG);
-    take(g.ro_rfl, 4ull * LG);
-    take(g.ro_dx, 4ull * (kP + 1));
+    take(g.ro_rfl, raw_db ? 4ull * LG : 0ull);
+    take(g.ro_dx, FS > 1 ? 4ull * (kP + 1) : 0ull);
     take(g.ro_lw, lin ? 4ull * FS * D : 0ull);
     take(g.ro_dlw, lin ? 4ull * FS * D : 0ull);
     take(g.ro_edge, 4ull * FS * (B + 1));
-    take(g.ro_cnt, 2ull * 2 * (kBlocks * FS * B + 1));
-    take(g.ro_seg, 4ull * (FS * B + 1));
+    take(g.ro_cnt, 2ull * kBlocks * cnt_stride(NK));
+    take(g.ro_seg, 4ull * (NK + 1));
     take(g.ro_tmp, 4ull * (kWideBlock / kWave));
+    if (FS == 1) g.ro_dx = -1;
     return take.off;
 }
 
@@ -1277,13 +1255,17 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                     geo.T = static_cast<int>((N + geo.NT - 1) / geo.NT);
                     geo.PM = PM;
                     geo.LGW = lgw;
-                    // chunks of sub-tiles: about PLE_TUNE_BWD_WG_PER_CU reduce
-                    // workgroups per CU, within the partials budget.  Two per
-                    // CU measured best at c1-c3 (4 per CU: +15 to +40 us, the
-                    // partials and each workgroup's table staging double)
+                    // chunks of sub-tiles: as many workgroups as the CUs
+                    // hold at once (registers allow two 256-thread or one
+                    // 512-thread workgroup per CU; LDS may allow fewer), so
+                    // that every workgroup starts in the first round, within
+                    // the partials budget.  More rounds (the
+                    // PLE_TUNE_BWD_WG_PER_CU knob) measured slower: each
+                    // workgroup stages its tables and writes its partials.
                     const int64_t per_chunk = F * B * 2 * D * 4;
+                    const int resident = rb == kWideBlock ? 1 : static_cast<int>(std::min<size_t>(2, kLdsMax / best_lds));
                     const int wg_k = tuning(PLE_TUNE_BWD_WG_PER_CU);
-                    int64_t c = (static_cast<int64_t>(wg_k > 0 ? wg_k : 2) * cus + geo.G - 1) / geo.G;
+                    int64_t c = (static_cast<int64_t>(wg_k > 0 ? wg_k : resident) * cus + geo.G - 1) / geo.G;
                     const int64_t budget_c = static_cast<int64_t>(kPartialBudget) / per_chunk;
                     if (c > budget_c) c = budget_c;
                     if (c > geo.T) c = geo.T;
@@ -1292,7 +1274,6 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                     pl.C = pl.Cd = (geo.T + geo.SPC - 1) / geo.SPC;
                     pl.NC = static_cast<int64_t>(geo.SPC) * geo.NT;
                     pl.geo = geo;
-                    pl.dxt_bytes = static_cast<size_t>(N) * F * sizeof(float);
                 }
             }
         }
@@ -1418,14 +1399,6 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
         a.idxb = idxb;
         e = launch_reduce<GD, Q>(a, pl.vec, epi, pl.rb, grid, pl.lds, s);
         if (e != hipSuccess) return e;
-        if (a.dxt) {
-            const dim3 tg(static_cast<unsigned>((a.N + kTr - 1) / kTr), static_cast<unsigned>((a.F + kTr - 1) / kTr));
-            const bool v4 = a.N % 4 == 0 && a.F % 4 == 0 && reinterpret_cast<uintptr_t>(a.dx) % 16 == 0;
-            if (v4) hipLaunchKernelGGL(ple_bwd_dx_transpose_kernel<true>, tg, dim3(kBlock), 0, s, a.dxt, a.dx, a.N, a.F);
-            else hipLaunchKernelGGL(ple_bwd_dx_transpose_kernel<false>, tg, dim3(kBlock), 0, s, a.dxt, a.dx, a.N, a.F);
-            e = hipGetLastError();
-            if (e != hipSuccess) return e;
-        }
     } else {
         if (want_dx) {
             const int64_t pairs = a.N * a.F;
@@ -1563,10 +1536,7 @@ int backward_run(const BackwardRequest &r) {
     a.part = want_dwdb ? part : nullptr;
     a.part_db = want_dwdb ? part_db : nullptr;
     a.part_lw = want_dwdb && lin ? part_lw : nullptr;
-    if (pl.sorted) {
-        float *dxt = reinterpret_cast<float *>(carve(pl.dxt_bytes));
-        a.dxt = want_dx ? dxt : nullptr;
-    }
+    if (!want_dx) a.dx = nullptr;
     a.N = r.N; a.F = static_cast<int>(r.F); a.B = static_cast<int>(r.B); a.D = static_cast<int>(r.D);
     a.C = pl.C; a.Cd = pl.Cd; a.NC = pl.NC;
     const int idxb = idx_bytes_for(r.B);

@@ -81,7 +81,9 @@ def test_noalloc_rejects_sizes_beyond_its_scratch():
     from piecewiselinearembeddings_optimized_amd import capi
 
     L = capi.lib()
-    n, f, bmax, d = 262144, 128, 48, 32          # about 0.5 GiB of workspace
+    # tables beyond LDS: the fallback's histogram cells live in the workspace,
+    # F * B * 2 D floats = 128 MiB
+    n, f, bmax, d = 1024, 64, 4096, 64
     assert L.ple_backward_workspace_bytes(n, f, bmax, d) > 64 << 20
     dummy = 256
     rc = L.ple_backward_launch_noalloc(*([dummy] * 7), dummy, dummy, dummy, n, f, bmax, d, 0, 0, None)
