@@ -17,12 +17,17 @@ forward+backward), fused against the reference's op sequence (the forward
 operator followed by PyTorch's linear0 and residual add).  ``--mode encode``
 times the dense encoding kernels (``encode`` / ``encode_backward``).
 
-Timing follows the reference harness's discipline (warm-up, then timed
-repetitions between device events on the stream the kernels run on).  The
-``roofline`` object prices the dominant kernel's algorithmic bytes per launch
-against MI355X's 8 TB/s HBM peak; ``cpu_baseline`` times the dense upstream
-CPU algorithm (``oracle/dense_torch.py``) on a bounded sample on the host
-cores.
+Timing: W untimed warm-up steps, then K steps between two events on the
+launch stream, synchronised on both sides (``value``, ``ms_per_step``); the
+same K steps again with each kernel's own start / end events (the library's
+``ple_timing_*``: hipExtLaunchKernelGGL records them at the kernel's start and
+end), which give the per-kernel durations of ``kernels`` and ``roofline``; and
+the reference harness's discipline, 10 repeats of 10 steps, median
+(``ms_per_step_median_10x10``).  ``roofline`` prices the dominant kernel's
+algorithmic bytes per launch against MI355X's 8 TB/s HBM peak;
+``cpu_baseline`` times the dense upstream CPU algorithm
+(``oracle/dense_torch.py``) on the job's host cores, on the whole batch where
+its dense [N, F, Bmax] intermediate stays within 1.6 GB, plus config 0.
 """
 
 from __future__ import annotations
@@ -47,7 +52,9 @@ def _parse():
     ap.add_argument("--version", choices=("A", "B"), default="B", help="module version (--mode module)")
     ap.add_argument("--activation", action="store_true", help="ReLU in the module (--mode module)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=4096, help="rows of the workload timed on the CPU")
+    ap.add_argument("--cpu-sample", type=int, default=None,
+                    help="rows of the workload timed on the CPU (default: the whole batch, up to a 1.6 GB "
+                         "dense intermediate)")
     return ap.parse_args()
 
 
@@ -60,22 +67,30 @@ def _traffic(kernel: str, workload: str):
         return json.load(fh).get("bytes_per_launch")
 
 
-def _cpu_baseline(w, n_rows: int):
+# dense [rows, F, Bmax] elements the CPU baseline's sample may hold (c1 in full:
+# 65536 x 128 x 48, a 1.6 GB fp32 intermediate)
+CPU_SAMPLE_ELEMS = 65536 * 128 * 48
+
+
+def _cpu_baseline(w, n_rows: int | None = None):
+    """The dense upstream algorithm on the host cores: fwd+bwd samples/s."""
     import numpy as np
     import torch
 
     from oracle.dense_torch import DensePLE
 
-    threads = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(threads)
-    rows = min(n_rows, w.x.shape[0])
+    # every core the job has (torch's default: OMP_NUM_THREADS where it is
+    # set -- 16 per GPU on the GPU boxes -- else all cores)
+    threads = torch.get_num_threads()
+    n, f, bmax, _ = w.shape
+    rows = min(n, max(1, CPU_SAMPLE_ELEMS // (f * bmax))) if n_rows is None else min(n_rows, n)
     x = torch.from_numpy(np.ascontiguousarray(w.x[:rows]))
-    g = torch.randn((rows, w.x.shape[1], w.weight.shape[2]), generator=torch.Generator().manual_seed(0))
+    g = torch.randn((rows, f, w.weight.shape[2]), generator=torch.Generator().manual_seed(0))
     m = DensePLE(w.bins, w.weight, w.bias)
-    for _ in range(2):
+    for _ in range(3):
         m.forward_backward(x, g)
     times = []
-    t_end = time.perf_counter() + 20.0
+    t_end = time.perf_counter() + 30.0
     while len(times) < 10 and (time.perf_counter() < t_end or len(times) < 3):
         t0 = time.perf_counter()
         m.forward_backward(x, g)
@@ -85,9 +100,11 @@ def _cpu_baseline(w, n_rows: int):
         "value": rows / med,
         "unit": "samples/s",
         "cores": threads,
+        "host_cpus": os.cpu_count(),
         "kind": "port",
-        "sample": f"{rows} of {w.x.shape[0]} rows of {w.name}, dense upstream algorithm in torch fp32 "
-                  f"(addcmul/clamp/cat/bmm/+bias, autograd fwd+bwd), median of {len(times)}",
+        "sample": f"{rows} of {n} rows of {w.name}, dense upstream algorithm in torch fp32 "
+                  f"(addcmul/clamp/cat/bmm/+bias, autograd fwd+bwd), 3 warm-up, median of {len(times)}",
+        "median_s": med,
     }
 
 
@@ -247,7 +264,7 @@ def main():
     import torch
 
     import piecewiselinearembeddings_optimized_amd  # noqa: F401  (registers the HIP ops)
-    from piecewiselinearembeddings_optimized_amd import workloads
+    from piecewiselinearembeddings_optimized_amd import capi, workloads
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     dev = torch.device("cuda:0")
@@ -283,7 +300,44 @@ def main():
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream()
-    # per-pass event timing on the launch stream
+
+    def region(steps, kernel_events):
+        """`steps` whole steps between two events on the launch stream,
+        synchronised on both sides; with kernel_events the library records an
+        event pair around the forward and the backward gradient kernel of
+        every step (ple_timing_*)."""
+        torch.cuda.synchronize()
+        if kernel_events:
+            capi.timing_start(steps)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        a.record(stream)
+        for _ in range(steps):
+            o, i = fwd()
+            if args.mode == "fwdbwd":
+                bwd(i)
+        b.record(stream)
+        torch.cuda.synchronize()
+        wall_s = time.perf_counter() - w0
+        kern = None
+        if kernel_events:
+            capi.timing_stop()
+            kern = {name: capi.timing_read(t) for name, t in
+                    (("fwd", capi.TIMER_FORWARD), ("bwd", capi.TIMER_BACKWARD))}
+            capi.timing_start(0)
+        return a.elapsed_time(b) / steps, wall_s, kern
+
+    # the timed region: K steps -> value
+    step_ms, wall, _ = region(args.steps, False)
+    value = n / (step_ms * 1e-3)
+    # the same K steps again with the kernels' own start / end events
+    # (hipExtLaunchKernelGGL) -> per-kernel durations for the roofline
+    instr_ms, _, kern = region(args.steps, True)
+    # the reference harness's discipline: 10 repeats x 10 steps, median
+    reps = sorted(region(10, False)[0] for _ in range(10))
+    median_ms = 0.5 * (reps[4] + reps[5])
+
+    # operator-level passes (the backward op includes its finalize kernel)
     def time_pass(fn, reps):
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
         for a, b in ev:
@@ -294,37 +348,26 @@ def main():
         ts = sorted(a.elapsed_time(b) for a, b in ev)
         return sum(ts) / len(ts), ts[len(ts) // 2]
 
-    fwd_avg_ms, fwd_med_ms = time_pass(fwd, args.steps)
+    fwd_op_ms, fwd_op_med = time_pass(fwd, args.steps)
     _, idx = fwd()
-    bwd_avg_ms = bwd_med_ms = 0.0
+    bwd_op_ms = bwd_op_med = 0.0
     if args.mode == "fwdbwd":
-        bwd_avg_ms, bwd_med_ms = time_pass(lambda: bwd(idx), args.steps)
-
-    # the timed region: K whole steps, synchronised on both sides
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    wall0 = time.perf_counter()
-    t0.record(stream)
-    for _ in range(args.steps):
-        out, idx = fwd()
-        if args.mode == "fwdbwd":
-            bwd(idx)
-    t1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    step_ms = t0.elapsed_time(t1) / args.steps
-    value = n / (step_ms * 1e-3)
+        bwd_op_ms, bwd_op_med = time_pass(lambda: bwd(idx), args.steps)
 
     fwd_bytes, bwd_bytes = workloads.algorithmic_bytes(n, f, bmax, d, out_bytes=out_bytes)
-    kernels = {
-        "ple_fwd_kernel": {"ms": fwd_avg_ms, "bytes": fwd_bytes},
-    }
-    if args.mode == "fwdbwd":
-        kernels["backward_op"] = {"ms": bwd_avg_ms, "bytes": bwd_bytes}
-    for k, v in kernels.items():
-        v["GB/s"] = v["bytes"] / (v["ms"] * 1e-3) / 1e9
-        v["frac"] = v["GB/s"] / HBM_PEAK_GBS
+    # the backward's gradient kernel writes no dW / db (its finalize does)
+    bwd_kernel_bytes = bwd_bytes - f * bmax * d * 4 - f * d * 4
+    kernels = {}
+    fwd_name = "ple_fwd_kernel"
+    bwd_name = "ple_bwd_fused_kernel"
+    for name, key, nbytes in ((fwd_name, "fwd", fwd_bytes), (bwd_name, "bwd", bwd_kernel_bytes)):
+        total_ms, launches = kern[key]
+        if launches == 0:
+            continue
+        avg = total_ms / launches
+        kernels[name] = {"ms": avg, "launches": launches, "bytes": nbytes,
+                         "GB/s": nbytes / (avg * 1e-3) / 1e9,
+                         "frac": nbytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
     dom_name = max(kernels, key=lambda k: kernels[k]["ms"])
     dom = kernels[dom_name]
     total_bytes = fwd_bytes + (bwd_bytes if args.mode == "fwdbwd" else 0)
@@ -332,6 +375,10 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         cpu = _cpu_baseline(w, args.cpu_sample)
+        if args.config != 0:
+            # the reference's CPU-runnable case too
+            c0 = _cpu_baseline(workloads.make(0))
+            cpu["c0_plumbing"] = {k: c0[k] for k in ("value", "unit", "cores", "sample", "median_s")}
 
     metric = ("fwd+bwd samples/s (B=65536,F=128,48 bins,d=32) + achieved HBM GB/s" if args.config == 1
               else f"{'fwd+bwd' if args.mode == 'fwdbwd' else 'fwd'} samples/s ({w.name})")
@@ -354,10 +401,12 @@ def main():
         },
         "achieved_GBps": total_bytes / (step_ms * 1e-3) / 1e9,
         "hbm_frac": total_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "fwd_ms": fwd_avg_ms,
-        "fwd_median_ms": fwd_med_ms,
-        "bwd_ms": bwd_avg_ms,
-        "bwd_median_ms": bwd_med_ms,
+        "ms_per_step_with_kernel_events": instr_ms,
+        "ms_per_step_median_10x10": median_ms,
+        "fwd_op_ms": fwd_op_ms,
+        "fwd_op_median_ms": fwd_op_med,
+        "bwd_op_ms": bwd_op_ms,
+        "bwd_op_median_ms": bwd_op_med,
         "kernels": kernels,
         "roofline": {
             "kernel": dom_name,
@@ -368,6 +417,7 @@ def main():
             "frac": dom["frac"],
             "traffic": _traffic(dom_name, w.name),
             "algorithmic_bytes": dom["bytes"],
+            "ms": dom["ms"],
         },
         "cpu_baseline": cpu,
         "wall_s_timed": wall,

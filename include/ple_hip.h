@@ -254,6 +254,28 @@ enum {
 };
 int ple_set_tuning(int knob, int value);
 
+/*
+ * Kernel timing, for benchmarks; no counterpart in the reference.  After
+ * ple_timing_start(slots), each of the next `slots` launches of the forward
+ * (resp. backward) entry points records a HIP event pair on its stream around
+ * its main kernel: PLE_TIMER_FORWARD brackets the forward kernel,
+ * PLE_TIMER_BACKWARD the backward's gradient kernel (the sorted-path kernel,
+ * or the fallback path's dx and histogram kernels), not the finalize that
+ * turns its partials into grad_weight / grad_bias.  ple_timing_read waits for
+ * the recorded pairs and returns their summed duration in milliseconds and
+ * their number.  ple_timing_stop ends recording; ple_timing_start(0) also
+ * releases the events.  The events belong to the device current at
+ * ple_timing_start.  Returns PLE_OK, PLE_E_* or a hipError_t.
+ */
+enum {
+    PLE_TIMER_FORWARD = 0,
+    PLE_TIMER_BACKWARD = 1,
+    PLE_TIMER_COUNT = 2,
+};
+int ple_timing_start(int slots);
+int ple_timing_stop(void);
+int ple_timing_read(int which, double *ms_total, int *count);
+
 /* Human-readable name of a return code (static storage). */
 const char *ple_error_string(int code);
 

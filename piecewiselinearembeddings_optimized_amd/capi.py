@@ -79,6 +79,10 @@ def lib() -> ctypes.CDLL:
         L.ple_encode_launch.restype = i32
         L.ple_encode_backward_launch.argtypes = [p, p, p, p, p, p, p, i64, i64, i64, i64, p]
         L.ple_encode_backward_launch.restype = i32
+        L.ple_timing_start.argtypes, L.ple_timing_start.restype = [i32], i32
+        L.ple_timing_stop.argtypes, L.ple_timing_stop.restype = [], i32
+        L.ple_timing_read.argtypes = [i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]
+        L.ple_timing_read.restype = i32
         _lib = L
     return _lib
 
@@ -87,6 +91,27 @@ def set_tuning(knob: str, value: int) -> int:
     """Sets planner override ``knob`` (a key of :data:`TUNE`); returns the
     previous value.  0 restores the planner's own choice."""
     return lib().ple_set_tuning(TUNE[knob], int(value))
+
+
+TIMER_FORWARD, TIMER_BACKWARD = 0, 1
+
+
+def timing_start(slots: int) -> None:
+    """``ple_timing_start``: time the main kernel of the next ``slots``
+    forward and backward launches (0 releases the events)."""
+    check(lib().ple_timing_start(int(slots)))
+
+
+def timing_stop() -> None:
+    check(lib().ple_timing_stop())
+
+
+def timing_read(which: int):
+    """``(total_ms, launches)`` recorded for ``TIMER_FORWARD`` / ``TIMER_BACKWARD``."""
+    ms = ctypes.c_double(0.0)
+    n = ctypes.c_int(0)
+    check(lib().ple_timing_read(int(which), ctypes.byref(ms), ctypes.byref(n)))
+    return ms.value, n.value
 
 
 def check(code: int) -> None:

@@ -312,10 +312,14 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
     constexpr int NTH = RB;
     constexpr bool kRelu = (EPI & kBwdRelu) != 0;
     constexpr bool kLin = (EPI & kBwdLin) != 0;
-    // With fp32 rounding and no linear0 branch the bias gradient is the sum of
-    // the bin buckets (taken at finalize); otherwise it needs its own sum of
-    // the unrounded (for linear0: unmasked) gradient.
-    constexpr bool kRawDb = Q != PLE_DTYPE_F32 || kLin;
+    // A gradient that arrives in the quantisation dtype (or fp32 rounding)
+    // is its own rounding: rounding it again changes nothing, and the bias
+    // gradient is then the sum of the bin buckets (taken at finalize).
+    // Otherwise -- an fp32 gradient rounded to 16 bits, or the linear0
+    // branch -- the bias gradient needs its own sum of the unrounded (for
+    // linear0: unmasked) gradient.
+    constexpr bool kGradExact = GD == Q || Q == PLE_DTYPE_F32;
+    constexpr bool kRawDb = !kGradExact || kLin;
     extern __shared__ __align__(16) unsigned char lds[];
     const int FS = a.FS, B = a.B, D = a.D, F = a.F, NT = a.NT;
     float *s_qw = reinterpret_cast<float *>(lds + a.ro_qw);             // [FS][B][D]
@@ -633,7 +637,7 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
                     gm[q] = __uint_as_float(__float_as_uint(gm[q]) &
                                             static_cast<uint32_t>(__builtin_amdgcn_sbfe(
                                                 static_cast<int>(mvi), m_shift + q, 1)));
-                gq[q] = quant<Q>(gm[q]);
+                gq[q] = kGradExact ? gm[q] : quant<Q>(gm[q]);
                 ab[q] += gq[q];
                 aw[q] = fmaf(qf, gq[q], aw[q]);
                 if constexpr (kRawDb) ad[q] += kLin ? gv[i][q] : gm[q];
@@ -1172,8 +1176,10 @@ size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_
     return take.off;
 }
 
-// g_align16: the gradient's base address is 16-byte aligned
-BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16, bool raw_db, bool lin) {
+// g_align16: the gradient's base address is 16-byte aligned; g16: the
+// gradient is a 16-bit type; raw_db: the bias gradient needs its own sums
+// (an fp32 gradient rounded to 16 bits, or linear0); lin: linear0 sums
+BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16, bool g16, bool raw_db, bool lin) {
     BwdPlan pl{};
     pl.rb = kBlock;
     const int cus = device_cu_count();
@@ -1229,7 +1235,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                 // linear0 branch): c2 -20 us; where two fit, the wide form
                 // measured slower (c3 +28 us, c4 +190 us).
                 {
-                    const bool wide_ok = !raw_db;
+                    const bool wide_ok = !raw_db && !g16;
                     bool wide = wide_ok && kLdsMax / best_lds < 2;
                     const int rb_env = tuning(PLE_TUNE_BWD_RB);
                     if (rb_env == kBlock || rb_env == kWideBlock) wide = wide_ok && rb_env == kWideBlock;
@@ -1304,7 +1310,8 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
 // Plans depend only on the shape, the gradient's alignment, the epilogue
 // flags, the device's CU count and the tuning knobs: a small per-thread cache
 // keeps the planner off the per-launch path.
-const BwdPlan &plan_cached(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16, bool raw_db, bool lin) {
+const BwdPlan &plan_cached(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16, bool g16, bool raw_db,
+                           bool lin) {
     struct Entry {
         int64_t N, F, B, D;
         int flags, cus;
@@ -1317,7 +1324,7 @@ const BwdPlan &plan_cached(int64_t N, int64_t F, int64_t B, int64_t D, bool g_al
     thread_local int next = 0;
     const int cus = device_cu_count();
     const uint32_t epoch = tuning_epoch();
-    const int flags = (g_align16 ? 1 : 0) | (raw_db ? 2 : 0) | (lin ? 4 : 0);
+    const int flags = (g_align16 ? 1 : 0) | (raw_db ? 2 : 0) | (lin ? 4 : 0) | (g16 ? 8 : 0);
     for (const Entry &e : cache)
         if (e.valid && e.N == N && e.F == F && e.B == B && e.D == D && e.flags == flags && e.cus == cus &&
             e.epoch == epoch)
@@ -1325,9 +1332,18 @@ const BwdPlan &plan_cached(int64_t N, int64_t F, int64_t B, int64_t D, bool g_al
     Entry &e = cache[next];
     next = (next + 1) % kEntries;
     e.N = N; e.F = F; e.B = B; e.D = D; e.flags = flags; e.cus = cus; e.epoch = epoch;
-    e.pl = plan_backward(N, F, B, D, g_align16, raw_db, lin);
+    e.pl = plan_backward(N, F, B, D, g_align16, g16, raw_db, lin);
     e.valid = true;
     return e.pl;
+}
+
+// Timer events of the backward's gradient kernels being issued
+// (launch_typed sets them; both NULL unless kernel timing is on).
+thread_local TimerSlot t_slot;
+
+template <typename K>
+void launch_bwd(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, const BwdArgs &a) {
+    hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), s, t_slot.start, t_slot.stop, 0u, a);
 }
 
 // Lane-group width as a template argument (DPP reductions) for the 4- and
@@ -1338,28 +1354,28 @@ hipError_t launch_reduce_epi(const BwdArgs &a, int vec, dim3 grid, size_t lds, h
     const dim3 blk(RB);
     if (vec == 4) {
         switch (a.LGW) {
-            case 2: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 4, 2, EPI, RB>), grid, blk, lds, s, a); break;
-            case 4: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 4, 4, EPI, RB>), grid, blk, lds, s, a); break;
-            case 8: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 4, 8, EPI, RB>), grid, blk, lds, s, a); break;
-            default: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 4, 16, EPI, RB>), grid, blk, lds, s, a); break;
+            case 2: launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 2, EPI, RB>), grid, blk, lds, s, a); break;
+            case 4: launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 4, EPI, RB>), grid, blk, lds, s, a); break;
+            case 8: launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 8, EPI, RB>), grid, blk, lds, s, a); break;
+            default: launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 16, EPI, RB>), grid, blk, lds, s, a); break;
         }
     } else if (vec == 2) {
         // (the planner takes 2 per lane for 6 <= D <= 64: groups of 4 to 32 lanes)
         switch (a.LGW) {
-            case 4: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 2, 4, EPI, RB>), grid, blk, lds, s, a); break;
-            case 8: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 2, 8, EPI, RB>), grid, blk, lds, s, a); break;
-            case 16: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 2, 16, EPI, RB>), grid, blk, lds, s, a); break;
-            case 32: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 2, 32, EPI, RB>), grid, blk, lds, s, a); break;
+            case 4: launch_bwd((ple_bwd_fused_kernel<GD, Q, 2, 4, EPI, RB>), grid, blk, lds, s, a); break;
+            case 8: launch_bwd((ple_bwd_fused_kernel<GD, Q, 2, 8, EPI, RB>), grid, blk, lds, s, a); break;
+            case 16: launch_bwd((ple_bwd_fused_kernel<GD, Q, 2, 16, EPI, RB>), grid, blk, lds, s, a); break;
+            case 32: launch_bwd((ple_bwd_fused_kernel<GD, Q, 2, 32, EPI, RB>), grid, blk, lds, s, a); break;
             default: return hipErrorInvalidConfiguration;
         }
     } else {
         // one column a lane: DPP group sums for the 16- to 64-lane groups
         // (9 <= D <= 64), shuffles at run time for the others
         switch (a.LGW) {
-            case 16: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 1, 16, EPI, RB>), grid, blk, lds, s, a); break;
-            case 32: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 1, 32, EPI, RB>), grid, blk, lds, s, a); break;
-            case 64: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 1, 64, EPI, RB>), grid, blk, lds, s, a); break;
-            default: hipLaunchKernelGGL((ple_bwd_fused_kernel<GD, Q, 1, 0, EPI, RB>), grid, blk, lds, s, a); break;
+            case 16: launch_bwd((ple_bwd_fused_kernel<GD, Q, 1, 16, EPI, RB>), grid, blk, lds, s, a); break;
+            case 32: launch_bwd((ple_bwd_fused_kernel<GD, Q, 1, 32, EPI, RB>), grid, blk, lds, s, a); break;
+            case 64: launch_bwd((ple_bwd_fused_kernel<GD, Q, 1, 64, EPI, RB>), grid, blk, lds, s, a); break;
+            default: launch_bwd((ple_bwd_fused_kernel<GD, Q, 1, 0, EPI, RB>), grid, blk, lds, s, a); break;
         }
     }
     return hipGetLastError();
@@ -1394,37 +1410,44 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
     hipError_t e = hipSuccess;
     const int epi = (a.mask ? kBwdRelu : 0) | (a.lin_w ? kBwdLin : 0);
     if (pl.sorted) {
-        a.db_from_buckets = Q == PLE_DTYPE_F32 && a.lin_w == nullptr;
+        a.db_from_buckets = (Q == PLE_DTYPE_F32 || GD == Q) && a.lin_w == nullptr;
         const dim3 grid(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, pl.C)));
         a.idxb = idxb;
+        t_slot = timer_slot(PLE_TIMER_BACKWARD);
         e = launch_reduce<GD, Q>(a, pl.vec, epi, pl.rb, grid, pl.lds, s);
+        t_slot = TimerSlot{};
         if (e != hipSuccess) return e;
     } else {
+        // timed from the start of the first kernel to the end of the last
+        const TimerSlot ts = timer_slot(PLE_TIMER_BACKWARD);
         if (want_dx) {
+            t_slot = TimerSlot{ts.start, want_dwdb ? nullptr : ts.stop};
             const int64_t pairs = a.N * a.F;
             int64_t blocks = (pairs + (kBlock / 16) - 1) / (kBlock / 16);
             const int64_t cap = static_cast<int64_t>(device_cu_count()) * 16;
             if (blocks > cap) blocks = cap;
             if (blocks < 1) blocks = 1;
-            if (idxb == 1) hipLaunchKernelGGL((ple_bwd_simple_dx_kernel<GD, Q, uint8_t>), dim3(blocks), dim3(kBlock), 0, s, a);
-            else if (idxb == 2) hipLaunchKernelGGL((ple_bwd_simple_dx_kernel<GD, Q, int16_t>), dim3(blocks), dim3(kBlock), 0, s, a);
-            else hipLaunchKernelGGL((ple_bwd_simple_dx_kernel<GD, Q, int32_t>), dim3(blocks), dim3(kBlock), 0, s, a);
+            if (idxb == 1) launch_bwd((ple_bwd_simple_dx_kernel<GD, Q, uint8_t>), dim3(blocks), dim3(kBlock), 0, s, a);
+            else if (idxb == 2) launch_bwd((ple_bwd_simple_dx_kernel<GD, Q, int16_t>), dim3(blocks), dim3(kBlock), 0, s, a);
+            else launch_bwd((ple_bwd_simple_dx_kernel<GD, Q, int32_t>), dim3(blocks), dim3(kBlock), 0, s, a);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
         if (want_dwdb) {
+            t_slot = TimerSlot{want_dx ? nullptr : ts.start, ts.stop};
             const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.F) * pl.C));
             if (pl.hist_global) {
-                if (idxb == 1) hipLaunchKernelGGL((ple_bwd_simple_hist_kernel<GD, Q, uint8_t, true>), grid, dim3(kWave), 0, s, a);
-                else if (idxb == 2) hipLaunchKernelGGL((ple_bwd_simple_hist_kernel<GD, Q, int16_t, true>), grid, dim3(kWave), 0, s, a);
-                else hipLaunchKernelGGL((ple_bwd_simple_hist_kernel<GD, Q, int32_t, true>), grid, dim3(kWave), 0, s, a);
+                if (idxb == 1) launch_bwd((ple_bwd_simple_hist_kernel<GD, Q, uint8_t, true>), grid, dim3(kWave), 0, s, a);
+                else if (idxb == 2) launch_bwd((ple_bwd_simple_hist_kernel<GD, Q, int16_t, true>), grid, dim3(kWave), 0, s, a);
+                else launch_bwd((ple_bwd_simple_hist_kernel<GD, Q, int32_t, true>), grid, dim3(kWave), 0, s, a);
             } else {
-                if (idxb == 1) hipLaunchKernelGGL((ple_bwd_simple_hist_kernel<GD, Q, uint8_t, false>), grid, dim3(kWave), pl.lds, s, a);
-                else hipLaunchKernelGGL((ple_bwd_simple_hist_kernel<GD, Q, int16_t, false>), grid, dim3(kWave), pl.lds, s, a);
+                if (idxb == 1) launch_bwd((ple_bwd_simple_hist_kernel<GD, Q, uint8_t, false>), grid, dim3(kWave), pl.lds, s, a);
+                else launch_bwd((ple_bwd_simple_hist_kernel<GD, Q, int16_t, false>), grid, dim3(kWave), pl.lds, s, a);
             }
             e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
+        t_slot = TimerSlot{};
     }
     if (want_dwdb) {
         size_t lds = static_cast<size_t>(a.B) * 2 * kFinStride * sizeof(float);
@@ -1488,11 +1511,12 @@ size_t backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D) {
         if (e.cus == cus && e.N == N && e.F == F && e.B == B && e.D == D && e.epoch == epoch) return e.bytes;
     size_t need = 0;
     for (int al = 0; al < 2; ++al)
-        for (int raw = 0; raw < 2; ++raw)
-            for (int lin = 0; lin <= raw; ++lin) {
-                const size_t t = plan_backward(N, F, B, D, al != 0, raw != 0, lin != 0).total();
-                need = t > need ? t : need;
-            }
+        for (int g16 = 0; g16 < 2; ++g16)
+            for (int raw = 0; raw < 2; ++raw)
+                for (int lin = 0; lin <= raw; ++lin) {
+                    const size_t t = plan_backward(N, F, B, D, al != 0, g16 != 0, raw != 0, lin != 0).total();
+                    need = t > need ? t : need;
+                }
     cache[next] = Entry{N, F, B, D, cus, epoch, need};
     next = (next + 1) % kEntries;
     return need;
@@ -1510,7 +1534,10 @@ int backward_run(const BackwardRequest &r) {
     const uintptr_t gaddr = reinterpret_cast<uintptr_t>(r.g);
     const int gbytes = r.grad_dtype == PLE_DTYPE_F32 ? 4 : 2;
     if (gaddr % gbytes != 0) return PLE_E_MISALIGNED;
-    const BwdPlan &pl = plan_cached(r.N, r.F, r.B, r.D, gaddr % 16 == 0, r.quant != PLE_DTYPE_F32 || lin, lin);
+    // (a gradient in the quantisation dtype is its own rounding: its bias
+    // gradient is the sum of the buckets, as for fp32)
+    const bool raw_db = (r.quant != PLE_DTYPE_F32 && r.quant != r.grad_dtype) || lin;
+    const BwdPlan &pl = plan_cached(r.N, r.F, r.B, r.D, gaddr % 16 == 0, r.grad_dtype != PLE_DTYPE_F32, raw_db, lin);
     // the sorted path always needs its descriptors; the fallback only for dW / db
     const size_t need = (pl.sorted || want_dwdb) ? pl.total() : 0;
     if (need > 0 && (r.workspace == nullptr || r.workspace_bytes < need ||

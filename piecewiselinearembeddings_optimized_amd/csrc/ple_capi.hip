@@ -2,6 +2,8 @@
 // no device, then the forward / backward launchers.
 
 #include <atomic>
+#include <mutex>
+#include <vector>
 
 #include "ple_internal.h"
 
@@ -30,6 +32,40 @@ std::atomic<uint32_t> g_tuning_epoch{0};
 int tuning(int knob) { return g_tuning[knob].load(std::memory_order_relaxed); }
 
 uint32_t tuning_epoch() { return g_tuning_epoch.load(std::memory_order_relaxed); }
+
+// Kernel timing: per timer, event pairs {begin, end} for up to `slots`
+// launches, recorded on the launch stream around the main kernel.
+namespace {
+
+struct Timer {
+    std::vector<hipEvent_t> ev;   // 2 * slots events: begin and end of launch i
+    int slots = 0;
+    int used = 0;
+};
+
+std::atomic<bool> g_timing{false};
+std::mutex g_timer_mu;
+Timer g_timers[PLE_TIMER_COUNT];
+
+void timers_release() {
+    for (Timer &t : g_timers) {
+        for (hipEvent_t e : t.ev) (void)hipEventDestroy(e);
+        t.ev.clear();
+        t.slots = t.used = 0;
+    }
+}
+
+}  // namespace
+
+TimerSlot timer_slot(int which) {
+    if (!g_timing.load(std::memory_order_relaxed)) return TimerSlot{};
+    std::lock_guard<std::mutex> lk(g_timer_mu);
+    Timer &t = g_timers[which];
+    if (t.used >= t.slots) return TimerSlot{};
+    const TimerSlot ts{t.ev[2 * t.used], t.ev[2 * t.used + 1]};
+    ++t.used;
+    return ts;
+}
 
 namespace {
 
@@ -71,6 +107,51 @@ int ple_set_tuning(int knob, int value) {
     const int prev = ple::g_tuning[knob].exchange(value, std::memory_order_relaxed);
     ple::g_tuning_epoch.fetch_add(1, std::memory_order_relaxed);
     return prev;
+}
+
+int ple_timing_start(int slots) {
+    if (slots < 0) return PLE_E_BAD_SHAPE;
+    std::lock_guard<std::mutex> lk(ple::g_timer_mu);
+    ple::g_timing.store(false, std::memory_order_relaxed);
+    ple::timers_release();
+    if (slots == 0) return PLE_OK;
+    for (ple::Timer &t : ple::g_timers) {
+        t.ev.resize(2 * static_cast<size_t>(slots), nullptr);
+        for (hipEvent_t &e : t.ev) {
+            const hipError_t rc = hipEventCreate(&e);
+            if (rc != hipSuccess) {
+                e = nullptr;
+                ple::timers_release();
+                return static_cast<int>(rc);
+            }
+        }
+        t.slots = slots;
+    }
+    ple::g_timing.store(true, std::memory_order_relaxed);
+    return PLE_OK;
+}
+
+int ple_timing_stop(void) {
+    ple::g_timing.store(false, std::memory_order_relaxed);
+    return PLE_OK;
+}
+
+int ple_timing_read(int which, double *ms_total, int *count) {
+    if (which < 0 || which >= PLE_TIMER_COUNT) return PLE_E_BAD_SHAPE;
+    if (!ms_total || !count) return PLE_E_NULL_POINTER;
+    std::lock_guard<std::mutex> lk(ple::g_timer_mu);
+    const ple::Timer &t = ple::g_timers[which];
+    double sum = 0.0;
+    for (int i = 0; i < t.used; ++i) {
+        hipError_t rc = hipEventSynchronize(t.ev[2 * i + 1]);
+        float ms = 0.0f;
+        if (rc == hipSuccess) rc = hipEventElapsedTime(&ms, t.ev[2 * i], t.ev[2 * i + 1]);
+        if (rc != hipSuccess) return static_cast<int>(rc);
+        sum += ms;
+    }
+    *ms_total = sum;
+    *count = t.used;
+    return PLE_OK;
 }
 
 const char *ple_error_string(int code) {

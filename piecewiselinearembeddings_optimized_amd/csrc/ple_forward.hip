@@ -99,7 +99,9 @@ __device__ __forceinline__ void emit_segment(const FwdArgs &a, float (&r)[VEC], 
     uint32_t mbits = 0;
 #pragma unroll
     for (int t2 = 0; t2 < VEC; ++t2) {
-        float o = quant<Q>(r[t2]);
+        // (with no epilogue the output dtype is Q, and the store's own
+        // rounding is this one)
+        float o = EPI == kEpiNone ? r[t2] : quant<Q>(r[t2]);
         if constexpr (HAS_BIAS) o = o + bvec[t2];
         if constexpr (RELU) {
             // torch.relu: NaN passes, x <= 0 gives 0
@@ -606,23 +608,32 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
     return true;
 }
 
+// Timer events of the forward launch being issued (forward_run sets them;
+// both NULL unless kernel timing is on).
+thread_local TimerSlot t_slot;
+
+template <typename K>
+void launch_fwd(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, const FwdArgs &a) {
+    hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), s, t_slot.start, t_slot.stop, 0u, a);
+}
+
 template <int Q, int OUT, int EPI, int VEC>
 hipError_t launch_idx(const FwdArgs &a, int idxb, bool wide, dim3 grid, size_t lds, hipStream_t s) {
     // uint8 indices up to 256 bins, int16 up to 32768, int32 beyond (those
     // tables never fit the table kernel's LDS)
     if (wide) {
-        if (idxb == 1) hipLaunchKernelGGL((ple_fwd_wide_kernel<Q, OUT, EPI, VEC, uint8_t>), grid, dim3(kWideFB), lds, s, a);
-        else if (idxb == 2) hipLaunchKernelGGL((ple_fwd_wide_kernel<Q, OUT, EPI, VEC, int16_t>), grid, dim3(kWideFB), lds, s, a);
-        else hipLaunchKernelGGL((ple_fwd_wide_kernel<Q, OUT, EPI, VEC, int32_t>), grid, dim3(kWideFB), lds, s, a);
+        if (idxb == 1) launch_fwd((ple_fwd_wide_kernel<Q, OUT, EPI, VEC, uint8_t>), grid, dim3(kWideFB), lds, s, a);
+        else if (idxb == 2) launch_fwd((ple_fwd_wide_kernel<Q, OUT, EPI, VEC, int16_t>), grid, dim3(kWideFB), lds, s, a);
+        else launch_fwd((ple_fwd_wide_kernel<Q, OUT, EPI, VEC, int32_t>), grid, dim3(kWideFB), lds, s, a);
         return hipGetLastError();
     }
     if (idxb == 4) return hipErrorInvalidConfiguration;
     if (a.FB == 2 * kBlock) {
-        if (idxb == 1) hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, uint8_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
-        else hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, int16_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
+        if (idxb == 1) launch_fwd((ple_fwd_kernel<Q, OUT, EPI, VEC, uint8_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
+        else launch_fwd((ple_fwd_kernel<Q, OUT, EPI, VEC, int16_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
     } else {
-        if (idxb == 1) hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, uint8_t, kBlock>), grid, dim3(kBlock), lds, s, a);
-        else hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, VEC, int16_t, kBlock>), grid, dim3(kBlock), lds, s, a);
+        if (idxb == 1) launch_fwd((ple_fwd_kernel<Q, OUT, EPI, VEC, uint8_t, kBlock>), grid, dim3(kBlock), lds, s, a);
+        else launch_fwd((ple_fwd_kernel<Q, OUT, EPI, VEC, int16_t, kBlock>), grid, dim3(kBlock), lds, s, a);
     }
     return hipGetLastError();
 }
@@ -633,11 +644,11 @@ hipError_t launch_vec(const FwdArgs &a, int vec, int idxb, bool wide, dim3 grid,
     if constexpr (OUT != PLE_DTYPE_F32 && EPI == kEpiNone) {
         if (vec == 8 && !wide) {
             if (a.FB == 2 * kBlock) {
-                if (idxb == 1) hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, 8, uint8_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
-                else hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, 8, int16_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
+                if (idxb == 1) launch_fwd((ple_fwd_kernel<Q, OUT, EPI, 8, uint8_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
+                else launch_fwd((ple_fwd_kernel<Q, OUT, EPI, 8, int16_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
             } else {
-                if (idxb == 1) hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, 8, uint8_t, kBlock>), grid, dim3(kBlock), lds, s, a);
-                else hipLaunchKernelGGL((ple_fwd_kernel<Q, OUT, EPI, 8, int16_t, kBlock>), grid, dim3(kBlock), lds, s, a);
+                if (idxb == 1) launch_fwd((ple_fwd_kernel<Q, OUT, EPI, 8, uint8_t, kBlock>), grid, dim3(kBlock), lds, s, a);
+                else launch_fwd((ple_fwd_kernel<Q, OUT, EPI, 8, int16_t, kBlock>), grid, dim3(kBlock), lds, s, a);
             }
             return hipGetLastError();
         }
@@ -689,6 +700,7 @@ int forward_run(const ForwardRequest &r) {
     if (grid > INT32_MAX) return PLE_E_TOO_LARGE;
     const int idxb = idx_bytes_for(r.B);
     hipError_t e;
+    t_slot = timer_slot(PLE_TIMER_FORWARD);
     switch (r.quant) {
         case PLE_DTYPE_F32: e = launch_q<PLE_DTYPE_F32>(a, epi, pl.vec, idxb, pl.wide, dim3(grid), pl.lds, r.stream); break;
         case PLE_DTYPE_F16: e = launch_q<PLE_DTYPE_F16>(a, epi, pl.vec, idxb, pl.wide, dim3(grid), pl.lds, r.stream); break;

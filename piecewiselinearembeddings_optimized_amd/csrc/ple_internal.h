@@ -1,6 +1,7 @@
 // Host-side interfaces between the translation units of libple_hip.so.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <stddef.h>
@@ -22,6 +23,16 @@ int tuning(int knob);
 // Changes whenever a tuning knob is set (plans cached under an older epoch
 // are stale).
 uint32_t tuning_epoch();
+
+// Kernel timing (ple_timing_*): the start / stop events of the next timed
+// launch of timer `which` (PLE_TIMER_*), or two NULLs when timing is off or
+// its slots are used up; the slot counts as used.  The events go to
+// hipExtLaunchKernelGGL, which records them at the kernel's start and end.
+struct TimerSlot {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+TimerSlot timer_slot(int which);
 
 inline int idx_bytes_for(int64_t B) { return B <= 256 ? 1 : (B <= 32768 ? 2 : 4); }
 

@@ -102,6 +102,24 @@ def test_ctypes_binding_declares_the_header_and_maps_errors():
     assert capi.workspace_bytes(2048, 4, 40000, 4) >= 4 * 40000 * 2 * 4 * 4
 
 
+def test_timing_api_without_a_device():
+    """Kernel timing: argument errors, and start(0) / stop / read with nothing
+    recorded need no device."""
+    import ctypes
+
+    from piecewiselinearembeddings_optimized_amd import capi
+
+    L = capi.lib()
+    assert L.ple_timing_start(-1) == -2
+    assert L.ple_timing_start(0) == 0
+    assert L.ple_timing_stop() == 0
+    ms, n = ctypes.c_double(1.0), ctypes.c_int(5)
+    assert L.ple_timing_read(2, ctypes.byref(ms), ctypes.byref(n)) == -2
+    assert L.ple_timing_read(0, None, ctypes.byref(n)) == -1
+    assert capi.timing_read(capi.TIMER_FORWARD) == (0.0, 0)
+    assert capi.timing_read(capi.TIMER_BACKWARD) == (0.0, 0)
+
+
 def test_tuning_knobs_round_trip():
     """Planner overrides: set, read back as the previous value, restored;
     unknown knobs rejected."""
