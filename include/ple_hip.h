@@ -230,7 +230,8 @@ int ple_encode_backward_launch(const float *grad_output, const float *x, const f
  *   PLE_TUNE_FWD_WIDE       1: the wide-table forward kernel for any shape
  *   PLE_TUNE_BWD_SIMPLE     1: the fallback backward kernels for any shape
  *   PLE_TUNE_BWD_SIMPLE_GLOBAL 1: their histogram cells in global memory
- *   PLE_TUNE_BWD_VEC        1: one gradient element per lane
+ *   PLE_TUNE_BWD_VEC        1: one gradient element per lane; 4: at most four
+ *                           (no 8-element lanes for 16-bit gradients)
  *   PLE_TUNE_BWD_FS         features per backward sub-tile (1, 2, 4, 8, 16)
  *   PLE_TUNE_BWD_RB         reducer threads per backward workgroup (256 or 512)
  *   PLE_TUNE_BWD_WG_PER_CU  backward workgroups per CU

@@ -179,6 +179,46 @@ __device__ __forceinline__ void load_grad_buf(__amdgpu_buffer_rsrc_t rs, uint32_
     }
 }
 
+// Dwords a lane holds for VEC gradient elements of a row: one per element for
+// fp32, two elements each for the 16-bit types, kept as loaded and widened at
+// use (grad_elem), so a 16-bit row costs half the registers of its floats.
+template <int G, int VEC>
+constexpr int grad_words() {
+    return G == PLE_DTYPE_F32 ? VEC : (VEC + 1) / 2;
+}
+
+template <int G, int VEC, int CPOL = 0>
+__device__ __forceinline__ void load_grad_words(__amdgpu_buffer_rsrc_t rs, uint32_t off,
+                                                uint32_t (&w)[grad_words<G, VEC>()]) {
+    constexpr int W = grad_words<G, VEC>();
+    if constexpr (W % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < W / 4; ++q) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * q, 0, CPOL);
+            w[4 * q] = v[0]; w[4 * q + 1] = v[1]; w[4 * q + 2] = v[2]; w[4 * q + 3] = v[3];
+        }
+    } else if constexpr (W == 2) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, CPOL);
+        w[0] = v[0]; w[1] = v[1];
+    } else if constexpr (G == PLE_DTYPE_F32 || VEC == 2) {
+        w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, CPOL);
+    } else {
+        w[0] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, CPOL);   // (low half)
+    }
+}
+
+// Element q (a compile-time index) of a row held as load_grad_words left it.
+template <int G>
+__device__ __forceinline__ float grad_elem(const uint32_t *w, int q) {
+    if constexpr (G == PLE_DTYPE_F32) {
+        return __uint_as_float(w[q]);
+    } else {
+        const uint32_t x = w[q >> 1];
+        if constexpr (G == PLE_DTYPE_BF16) return __uint_as_float((q & 1) ? (x & 0xffff0000u) : (x << 16));
+        else return f16_to_float(static_cast<uint16_t>((q & 1) ? (x >> 16) : x));
+    }
+}
+
 // VEC consecutive floats from / to LDS (16-byte accesses for VEC 4 and 8,
 // 8-byte for VEC 2; the address is aligned to the access in those cases).
 template <int VEC>

@@ -598,6 +598,15 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
         const int64_t min_nc = (static_cast<int64_t>(kOutPerTable) * B * 4 + out_bytes - 1) / out_bytes;
         const int64_t c_tbl = (N + min_nc - 1) / min_nc;
         if (c > c_tbl) c = c_tbl;
+        // Tables that leave room for at most two workgroups per CU: exactly
+        // two rounds of resident workgroups, so the last round is as full as
+        // the first (fwd+bwd step, its forward: c3 156 -> 140 us, c2 58 -> 57
+        // us, c4 165 -> 159 us, against 1.6 to 3.2 rounds before)
+        if (kLdsMax / pl.lds <= 2) {
+            const int64_t slots = static_cast<int64_t>(kLdsMax / pl.lds) * device_cu_count();
+            c = (2 * slots) / pl.G;
+            if (c < 1) c = 1;
+        }
     }
     const int64_t sw = kWave / fs;
     const int64_t max_c = (N + sw - 1) / sw;          // at least one wave tile per chunk
