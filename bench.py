@@ -17,12 +17,13 @@ forward+backward), fused against the reference's op sequence (the forward
 operator followed by PyTorch's linear0 and residual add).  ``--mode encode``
 times the dense encoding kernels (``encode`` / ``encode_backward``).
 
-Timing: W untimed warm-up steps, then K steps between two events on the
-launch stream, synchronised on both sides (``value``, ``ms_per_step``); the
-same K steps again with each kernel's own start / end events (the library's
-``ple_timing_*``: hipExtLaunchKernelGGL records them at the kernel's start and
-end), which give the per-kernel durations of ``kernels`` and ``roofline``; and
-the reference harness's discipline, 10 repeats of 10 steps, median
+Timing: W untimed warm-up steps; the forward and backward operators timed
+alone (K calls each); K steps with each kernel's own start / end events (the
+library's ``ple_timing_*``: hipExtLaunchKernelGGL records them at the
+kernel's start and end), which give the per-kernel durations of ``kernels``
+and ``roofline``; then the timed region -- K whole steps between two events on the launch
+stream, synchronised on both sides (``value``, ``ms_per_step``) -- and the
+reference harness's discipline, 10 repeats of 10 steps, median
 (``ms_per_step_median_10x10``).  ``roofline`` prices the dominant kernel's
 algorithmic bytes per launch against MI355X's 8 TB/s HBM peak;
 ``cpu_baseline`` times the dense upstream CPU algorithm
@@ -327,16 +328,6 @@ def main():
             capi.timing_start(0)
         return a.elapsed_time(b) / steps, wall_s, kern
 
-    # the timed region: K steps -> value
-    step_ms, wall, _ = region(args.steps, False)
-    value = n / (step_ms * 1e-3)
-    # the same K steps again with the kernels' own start / end events
-    # (hipExtLaunchKernelGGL) -> per-kernel durations for the roofline
-    instr_ms, _, kern = region(args.steps, True)
-    # the reference harness's discipline: 10 repeats x 10 steps, median
-    reps = sorted(region(10, False)[0] for _ in range(10))
-    median_ms = 0.5 * (reps[4] + reps[5])
-
     # operator-level passes (the backward op includes its finalize kernel)
     def time_pass(fn, reps):
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
@@ -353,6 +344,17 @@ def main():
     bwd_op_ms = bwd_op_med = 0.0
     if args.mode == "fwdbwd":
         bwd_op_ms, bwd_op_med = time_pass(lambda: bwd(idx), args.steps)
+
+    # K steps with the kernels' own start / end events (hipExtLaunchKernelGGL)
+    # -> per-kernel durations inside the step, for the roofline
+    instr_ms, _, kern = region(args.steps, True)
+    # the timed region: K whole steps, no kernel events -> value (after the
+    # passes above, so the GPU's clocks have settled however short W is)
+    step_ms, wall, _ = region(args.steps, False)
+    value = n / (step_ms * 1e-3)
+    # the reference harness's discipline: 10 repeats x 10 steps, median
+    reps = sorted(region(10, False)[0] for _ in range(10))
+    median_ms = 0.5 * (reps[4] + reps[5])
 
     fwd_bytes, bwd_bytes = workloads.algorithmic_bytes(n, f, bmax, d, out_bytes=out_bytes)
     # the backward's gradient kernel writes no dW / db (its finalize does)
