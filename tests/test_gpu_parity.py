@@ -289,6 +289,8 @@ SHAPES = [
     (600, 3, 25, 23), (450, 2, 70, 31), (350, 4, 12, 9),
     # wider ones: two columns a lane in 32-lane groups, one column a lane in 64-lane groups
     (700, 3, 30, 38), (400, 3, 15, 62), (500, 2, 20, 47),
+    # the forward's 512-thread plans of rows up to 24 columns with up to 8 features a group
+    (2048, 128, 48, 24), (2048, 128, 48, 12),
 ]
 
 
@@ -329,6 +331,28 @@ def test_two_column_lanes_16bit(d, quant, c_oracle):
     gx, gw = ops.backward(g_h.to(DEV), x, e, iw, nb, wt, idx, True, True)
     torch.cuda.synchronize()
     _check_backward(w, quant, g_h.float().numpy(), gx, gw, None, c_oracle)
+
+
+@pytest.mark.parametrize("d", [8, 16, 40, 64])
+@pytest.mark.parametrize("quant", ["bf16", "f16"])
+def test_eight_column_lanes_16bit(d, quant, c_oracle, tune):
+    """16-bit gradients with D a multiple of 8: eight columns a lane, rows kept
+    packed in registers (lane groups of 2, 2, 8 and 8 lanes), with rows on
+    their bins' left edges among them; against the quantisation-aware float64
+    oracle, as is the four-column form of the same call (knob BWD_VEC=4)."""
+    n, f, bmax = 1300, 3, 37
+    w = _random_case(n, f, bmax, d, seed=d + 101)
+    print(f"eight-column lanes {w.name} {quant}", flush=True)
+    x, e, iw, nb, wt, bt = _inputs(w)
+    out, idx = ops.forward(x, e, iw, nb, wt, QUANT_TORCH[quant])
+    g_h = torch.from_numpy(_grad((n, f, d), d + 3)).to(QUANT_TORCH[quant])
+    gx, gw = ops.backward(g_h.to(DEV), x, e, iw, nb, wt, idx, True, True)
+    torch.cuda.synchronize()
+    _check_backward(w, quant, g_h.float().numpy(), gx, gw, None, c_oracle)
+    tune("BWD_VEC", 4)
+    gx4, gw4 = ops.backward(g_h.to(DEV), x, e, iw, nb, wt, idx, True, True)
+    torch.cuda.synchronize()
+    _check_backward(w, quant, g_h.float().numpy(), gx4, gw4, None, c_oracle)
 
 
 @pytest.mark.parametrize("d", [10, 30])
