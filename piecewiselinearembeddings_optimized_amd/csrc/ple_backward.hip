@@ -308,7 +308,7 @@ __device__ __forceinline__ void tile_place(const BwdArgs &a, int tid, const int 
 // ---------------------------------------------------------------------------
 
 template <int GD, int Q, int VEC, int LGW_T, int EPI, int RB>
-__global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
+__global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     constexpr int NTH = RB;
     constexpr bool kRelu = (EPI & kBwdRelu) != 0;
     constexpr bool kLin = (EPI & kBwdLin) != 0;
@@ -633,12 +633,17 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
             if constexpr (kRelu) return kQuadEpi ? quad_bcast(mv[0], i) : mv[i];
             else return 0u;
         };
+        // The edge term: a second pass over the registers that a wave takes
+        // only when it holds an edge row, for the plain kernels; the module
+        // epilogues' kernels fold it into the first pass (a second pass
+        // there takes them past 256 VGPRs, one wave per SIMD).
+        constexpr bool kEdgePass = !kRelu && !kLin;
         float parts[kL];
         bool edge = false;
 #pragma unroll
         for (int i = 0; i < kL; ++i) {
             const float qf = __uint_as_float(dsc[i].x);
-            float dot = 0.0f, dotl = 0.0f;
+            float dot = 0.0f, dotl = 0.0f, dot2 = 0.0f;
             const uint32_t mvi = mask_word(i);
             float xvi = 0.0f;
             if constexpr (kLin) xvi = kQuadEpi ? __uint_as_float(quad_bcast(__float_as_uint(xv[0]), i)) : xv[i];
@@ -655,16 +660,19 @@ __global__ __launch_bounds__(RB) void ple_bwd_fused_kernel(BwdArgs a) {
                     dotl = fmaf(graw, lw[q], dotl);
                 }
                 dot = fmaf(gq, wk[q], dot);
+                if constexpr (!kEdgePass) dot2 = fmaf(gq, wp[q], dot2);
             }
             float part = dot * iwk;
             if constexpr (kLin) part += dotl;
+            // x on the bin's left edge (k >= 1, marked by q(frac) = -0): the
+            // lower bin's term too
+            if constexpr (!kEdgePass) part = dsc[i].x == 0x80000000u ? fmaf(dot2, iwp, part) : part;
             parts[i] = part;
             edge = edge || dsc[i].x == 0x80000000u;
         }
-        // x on the bin's left edge (k >= 1, marked by q(frac) = -0): the
-        // lower bin's term too.  Such rows are rare in most data: the wave
-        // takes this branch only when one of its lane groups holds one.
-        if (__any(edge)) {
+        // Edge rows are rare in most data: the wave takes this branch only
+        // when one of its lane groups holds one.
+        if (kEdgePass && __any(edge)) {
 #pragma unroll
             for (int i = 0; i < kL; ++i) {
                 const uint32_t mvi = mask_word(i);
