@@ -1229,8 +1229,9 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
         if (vec == 1 && g_align16 && D % 2 == 0 && D >= 6 && D <= 64) vec = 2;
         // 16-bit gradients: 8 elements (one 16-byte load) a lane when D
         // allows; the row stays packed in 4 registers, so the per-row work of
-        // a lane group covers twice the columns (with the edge-term branch
-        // below: c4 backward 296 -> 282 us in the fwd+bwd step)
+        // a lane group covers twice the columns (with the edge term's
+        // separate pass in the reduce: c4 backward 296 -> 282 us in the
+        // fwd+bwd step)
         if (g16 && g_align16 && D % 8 == 0 && tuning(PLE_TUNE_BWD_VEC) != 4) vec = 8;
         if (tuning(PLE_TUNE_BWD_VEC) == 1) vec = 1;
         const int uv = static_cast<int>(D / vec);
