@@ -137,3 +137,48 @@ def test_c_abi_rejects_before_launch_on_device(capi):
         capi.backward(g.to(torch.bfloat16), x, e, iw, nb, wt, idx, None, gw, None, torch.float32)
     assert ei.value.code == -7
     torch.cuda.synchronize()
+
+
+def test_kernel_timing_counts_launches(capi):
+    """ple_timing_*: each forward and backward launch within the slots records
+    one event pair around its main kernel (sorted path and fallback path);
+    launches past the slots and after ple_timing_stop record nothing, and the
+    results are unchanged by the timing."""
+    w = workloads.make(1, 2048)
+    n, f, bmax, d = w.shape
+    x, e, iw, nb, wt = _t(w.x), _t(w.edges), _t(w.inv_widths), _t(w.n_bins), _t(w.weight)
+    out = torch.empty((n, f, d), device=DEV)
+    idx = torch.empty((n, f), dtype=torch.uint8, device=DEV)
+    g = torch.randn((n, f, d), device=DEV, generator=torch.Generator(DEV).manual_seed(3))
+    grads = [torch.empty((n, f), device=DEV), torch.empty_like(wt), torch.empty((f, d), device=DEV)]
+    capi.forward(x, e, iw, nb, wt, None, out, idx, torch.float32)
+    capi.backward(g, x, e, iw, nb, wt, idx, *grads, torch.float32)
+    torch.cuda.synchronize()
+    ref = [t.clone() for t in grads]
+    try:
+        capi.timing_start(2)
+        for _ in range(3):      # the third launch of each finds no slot left
+            capi.forward(x, e, iw, nb, wt, None, out, idx, torch.float32)
+            capi.backward(g, x, e, iw, nb, wt, idx, *grads, torch.float32)
+        capi.set_tuning("BWD_SIMPLE", 1)     # the fallback kernels are timed as one span
+        capi.timing_start(1)
+        capi.backward(g, x, e, iw, nb, wt, idx, *grads, torch.float32)
+        torch.cuda.synchronize()
+        ms_b, cnt_b = capi.timing_read(capi.TIMER_BACKWARD)
+        assert cnt_b == 1 and ms_b > 0.0
+        capi.set_tuning("BWD_SIMPLE", 0)
+        capi.timing_start(2)
+        capi.forward(x, e, iw, nb, wt, None, out, idx, torch.float32)
+        capi.backward(g, x, e, iw, nb, wt, idx, *grads, torch.float32)
+        capi.timing_stop()
+        capi.forward(x, e, iw, nb, wt, None, out, idx, torch.float32)
+        torch.cuda.synchronize()
+        for which in (capi.TIMER_FORWARD, capi.TIMER_BACKWARD):
+            ms, cnt = capi.timing_read(which)
+            print(f"  timer {which}: {cnt} launches, {ms:.4f} ms", flush=True)
+            assert cnt == 1 and 0.0 < ms < 100.0
+    finally:
+        capi.set_tuning("BWD_SIMPLE", 0)
+        capi.timing_start(0)
+    for got, want in zip(grads, ref):
+        assert torch.equal(got, want)
