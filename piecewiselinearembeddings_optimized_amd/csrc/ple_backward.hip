@@ -84,6 +84,7 @@ struct BwdArgs {
     int db_from_buckets;   // finalize: db = sum of the bin buckets (no raw-gradient partials)
     int fin_direct;        // finalize: chunk sums read straight from the partials (no LDS table)
     int fin_summed;        // finalize: the chunk partials are summed into chunk 0 already
+    int fin_fused;         // sorted path, one chunk: dW / db straight from the LDS histogram (no finalize kernel)
     int idxb;              // bytes per bin index (1 or 2 on the sorted path)
     // sorted path
     int FS, G, NT, T, SPC, PM, LGW;   // T sub-tiles, SPC sub-tiles per chunk, PM piece capacity
@@ -103,6 +104,15 @@ constexpr int kWideBlock = 2 * kBlock;
 
 constexpr int kBwdRelu = 1;
 constexpr int kBwdLin = 2;
+
+// finalize (dW / db from the chunk partials): one workgroup per (feature,
+// group of kFinCols columns), kFinLanes lanes per column
+constexpr int kFinCols = 8;
+// LDS row stride of the chunk-sum table: one more than kFinCols, so that the
+// lanes of a column (consecutive bins) read distinct banks
+constexpr int kFinStride = kFinCols + 1;
+constexpr int kFinLoadsInline = 128;   // chunk-sum loads per finalize thread, at most
+constexpr int kFinLanes = kBlock / kFinCols;   // lanes per column (half a wave)
 
 // ---------------------------------------------------------------------------
 // sub-tile sort (all threads of the fused kernel, between reduce phases)
@@ -861,6 +871,59 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     }
     __syncthreads();
 
+    // One chunk: this workgroup has seen every sample of its features, so it
+    // writes dW and db from the LDS histogram itself, with the finalize
+    // kernel's steps and lane count (the results repeat those of the
+    // two-kernel path bitwise): kFinLanes lanes per column, columns in turn,
+    // each lane sums the buckets of its run of bins, a suffix scan over the
+    // lanes gives every run the sum of the runs above it, and each lane walks
+    // its run from the top, dW[phys k] = weighted[k] + sum_{m > k} bucket[m];
+    // slots no bin maps to get 0.  Whole lane groups run every pass (a group
+    // past the live columns scans zeros), so the shuffles see live lanes.
+    if (a.fin_fused) {
+        constexpr int kGroups = NTH / kFinLanes;
+        const int l = tid % kFinLanes;
+        const int D2 = 2 * D;
+        for (int col0 = 0; col0 < nfh * D; col0 += kGroups) {
+            const int col = col0 + tid / kFinLanes;
+            const bool ok = col < nfh * D;
+            const int fl = ok ? col / D : 0;
+            const int j = ok ? col - fl * D : 0;
+            const int n = ok ? s_nb[fl] : 0;
+            const float *h = s_hist + static_cast<size_t>(fl) * B * D2 + j;   // bucket at k * D2, weighted at + D
+            const int m = (n + kFinLanes - 1) / kFinLanes;
+            const int lo = min(n, l * m);
+            const int hi = min(n, lo + m);
+            float run = 0.0f;
+            for (int k = hi - 1; k >= lo; --k) run += h[k * D2];
+            float incl = run;
+#pragma unroll
+            for (int off = 1; off < kFinLanes; off <<= 1) {
+                const float t = __shfl_down(incl, off, kFinLanes);
+                if (l + off < kFinLanes) incl += t;
+            }
+            const float above = __shfl_down(incl, 1, kFinLanes);
+            if (!ok) continue;
+            const int64_t wrow = static_cast<int64_t>(f0 + fl) * B;
+            if (a.dw) {
+                float fut = l + 1 < kFinLanes ? above : 0.0f;
+                for (int k = hi - 1; k >= lo; --k) {
+                    a.dw[(wrow + phys_bin(k, n, B)) * D + j] = h[k * D2 + D] + fut;
+                    fut += h[k * D2];
+                }
+                for (int k = n - 1 + l; k < B - 1; k += kFinLanes) a.dw[(wrow + k) * D + j] = 0.0f;
+            }
+            if (l == 0) {
+                const int64_t fj = static_cast<int64_t>(f0 + fl) * D + j;
+                if (a.db) a.db[fj] = a.db_from_buckets ? incl : s_db[fl * D + j];
+                if constexpr (kLin) {
+                    if (a.dlw) a.dlw[fj] = s_dlw[fl * D + j];
+                }
+            }
+        }
+        return;
+    }
+
     // chunk partials
     if (a.part) {
         const int D2 = 2 * D;
@@ -1049,11 +1112,6 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_chunksum_kernel(float *part, i
 // finalize: one workgroup per (feature, group of kFinCols columns)
 // ---------------------------------------------------------------------------
 
-constexpr int kFinCols = 8;
-// LDS row stride of the chunk-sum table: one more than kFinCols, so that the
-// lanes of a column (consecutive bins) read distinct banks
-constexpr int kFinStride = kFinCols + 1;
-constexpr int kFinLoadsInline = 128;   // chunk-sum loads per finalize thread, at most
 
 // Sums the chunk partials of every (bin, column) of the group in chunk order
 // into LDS (or reads their sums from chunk 0, where ple_bwd_chunksum_kernel
@@ -1064,7 +1122,6 @@ constexpr int kFinLoadsInline = 128;   // chunk-sum loads per finalize thread, a
 // sum above it, and each lane walks its run from the top.  Slots no bin maps
 // to get 0.  The bias gradient is the sum of all buckets (fp32 gradients) or
 // its own summed partials.  A fixed order throughout: results repeat bitwise.
-constexpr int kFinLanes = kBlock / kFinCols;   // lanes per column (half a wave)
 
 __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
     extern __shared__ float tot[];       // [n][2][kFinStride]
@@ -1464,6 +1521,8 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
         a.db_from_buckets = (Q == PLE_DTYPE_F32 || GD == Q) && a.lin_w == nullptr;
         const dim3 grid(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, pl.C)));
         a.idxb = idxb;
+        // one chunk: the gradient kernel writes dW / db itself
+        a.fin_fused = want_dwdb && pl.C == 1;
         t_slot = timer_slot(PLE_TIMER_BACKWARD);
         e = launch_reduce<GD, Q>(a, pl.vec, epi, pl.rb, grid, pl.lds, s);
         t_slot = TimerSlot{};
@@ -1500,7 +1559,7 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
         }
         t_slot = TimerSlot{};
     }
-    if (want_dwdb) {
+    if (want_dwdb && !(pl.sorted && a.fin_fused)) {
         size_t lds = static_cast<size_t>(a.B) * 2 * kFinStride * sizeof(float);
         a.fin_direct = lds > kLdsMax;          // very many bins: no LDS table
         if (a.fin_direct) lds = 0;

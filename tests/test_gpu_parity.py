@@ -372,6 +372,43 @@ def test_two_column_lanes_match_one_column_lanes(d, c_oracle, tune):
     _check_backward(w, "f32", g, gx, gw, gb, c_oracle)
 
 
+@pytest.mark.parametrize("quant", ["f32", "bf16"])
+def test_single_chunk_plan_writes_dw_db_in_kernel(quant, c_oracle, tune):
+    """Plans with one chunk of samples (one feature a workgroup over 600
+    features, or a batch of one sub-tile) take dW and db from the gradient
+    kernel's own histogram, with no partials and no finalize kernel; a plan
+    of several chunks (knob BWD_WG_PER_CU=8) takes the two-kernel route.
+    Both against the float64 oracle (bf16: an fp32 gradient rounded for
+    dx/dW, db from the unrounded gradient), every output element written
+    (the buffers start as NaN), padding weight slots exactly zero."""
+    from piecewiselinearembeddings_optimized_amd import capi
+
+    qt = QUANT_TORCH[quant]
+    for n, f in ((3000, 600), (700, 9)):
+        bmax, d = 20, 8
+        w = _random_case(n, f, bmax, d, seed=n + f)
+        print(f"single-chunk plan {w.name} n={n} f={f} {quant}", flush=True)
+        x, e, iw, nb, wt, bt = _inputs(w)
+        _, idx = ops.forward_with_bias(x, e, iw, nb, wt, bt, qt)
+        g = _grad((n, f, d), n)
+        gd = _t(g)
+        tune("BWD_FS", 1)
+        for wg in (0, 8):
+            tune("BWD_WG_PER_CU", wg)
+            gx = torch.full((n, f), float("nan"), device=DEV)
+            gw = torch.full(tuple(wt.shape), float("nan"), device=DEV)
+            gb = torch.full((f, d), float("nan"), device=DEV)
+            capi.backward(gd, x, e, iw, nb, wt, idx, gx, gw, gb, qt)
+            torch.cuda.synchronize()
+            gq = po.quantize(g, quant) if quant != "f32" else g
+            _check_backward(w, quant, gq, gx, gw, gb, c_oracle, grad_bias_source=g if quant != "f32" else None)
+            for j in range(f):   # the last bin sits in slot bmax-1; slots n-1 .. bmax-2 are padding
+                assert torch.count_nonzero(gw[j, max(int(w.n_bins[j]), 1) - 1:bmax - 1]) == 0
+            if n <= 1024:   # one sub-tile: one chunk whatever the knob
+                break
+        tune("BWD_WG_PER_CU", 0)
+
+
 @pytest.mark.parametrize("cfg", [0, 1, 2, 3])
 def test_fallback_backward_path_matches_oracle(cfg, c_oracle, tune):
     """The simple (non-fused) backward kernels, forced by the BWD_SIMPLE knob."""
