@@ -131,6 +131,9 @@ __device__ __forceinline__ void emit_segment(const FwdArgs &a, float (&r)[VEC], 
 template <int Q, int OUT, int EPI, int VEC, typename IdxT, int FB>
 __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
     constexpr int kWaves = FB / kWave;
+    // wave tiles whose x is loaded during the table staging: with 512
+    // threads (short output rows) all of a wave's tiles in the usual plans
+    constexpr int kXEarly = FB == 512 ? 16 : 1;
     constexpr bool HAS_BIAS = EPI == kEpiBias || EPI == kEpiBiasRelu;
     constexpr bool LIN = EPI == kEpiLin || EPI == kEpiLinRelu;
     extern __shared__ float smem[];
@@ -149,6 +152,21 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
     const int64_t n_end = min(a.N, n_begin + a.NC);
     if (n_begin >= n_end) return;
     const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    const int SW = kWave / FS;      // samples per wave tile
+    const int64_t n_tiles = (n_end - n_begin + SW - 1) / SW;
+    // pair phase: lane -> (sample p_s, feature p_fl)
+    const int p_s = lane / FS;
+    const int p_fl = lane - p_s * FS;
+    const bool p_fok = p_fl < nfh;
+    // x of wave tile t (an out-of-range lane reads x[0] and ignores it, so
+    // the load has no branch around it)
+    auto load_x = [&](int64_t t) __attribute__((always_inline)) -> float {
+        const int64_t pn = n_begin + t * SW + p_s;
+        const bool ok = p_fok && (t < n_tiles) && (pn < n_end);
+        return a.x[ok ? pn * F + f0 + p_fl : 0];
+    };
 
     // ---- stage the per-feature tables ------------------------------------
     for (int i = tid; i < FS; i += FB) snb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
@@ -190,6 +208,13 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
             }
         }
     }
+    // x of the wave's first kXEarly tiles, loaded while the tables are
+    // staged: after a kernel that streamed other data through the caches, x
+    // comes from memory, and with short rows (16-bit or narrow outputs, 512
+    // threads) a tile's stores take less time than that load
+    float x_early[kXEarly];
+#pragma unroll
+    for (int i = 0; i < kXEarly; ++i) x_early[i] = load_x(wave + static_cast<int64_t>(i) * kWaves);
     __syncthreads();
 
     // prefix over logical bins, one lane per (feature, column), in bin order
@@ -221,19 +246,12 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
     __syncthreads();
 
     // ---- stream wave tiles -------------------------------------------------
-    const int wave = tid / kWave;
-    const int lane = tid % kWave;
-    const int SW = kWave / FS;      // samples per wave tile
     const int Lv = FS * U;          // vector slots per sample row of the group
     const int R = kWave / Lv;       // sample rows per store instruction
 
-    // pair phase: lane -> (sample p_s, feature p_fl)
-    const int p_s = lane / FS;
-    const int p_fl = lane - p_s * FS;
     const float *e_row = sedge + p_fl * (B + 1);
     const float *iw_row = siw + p_fl * B;
     const int p_n = snb[p_fl];
-    const bool p_fok = p_fl < nfh;
 
     // store phase: lane -> (row o_s, feature o_fl, vector o_u), fixed per lane
     const int o_s = lane / Lv;
@@ -261,27 +279,15 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
     const int m_word = (o_u * VEC) >> 5;
     const float *o_tbl = tbl + static_cast<size_t>(o_fl) * B * rs + o_u * VEC;
 
-    const int64_t rows = n_end - n_begin;
-    const int64_t n_tiles = (rows + SW - 1) / SW;
     const int64_t row_elems = static_cast<int64_t>(F) * D;
 
-    // x of the wave's next tile is loaded while the current tile is stored
-    // (an out-of-range lane reads x[0] and ignores it, so the load has no
-    // branch around it)
-    auto load_x = [&](int64_t t) __attribute__((always_inline)) -> float {
-        const int64_t pn = n_begin + t * SW + p_s;
-        const bool ok = p_fok && (t < n_tiles) && (pn < n_end);
-        return a.x[ok ? pn * F + f0 + p_fl : 0];
-    };
-    float v_next = load_x(wave);
-
-    for (int64_t t = wave; t < n_tiles; t += kWaves) {
+    // one wave tile: bin search, bin index, and the tile's output rows
+    auto tile = [&](int64_t t, float xv) __attribute__((always_inline)) {
         const int64_t n0 = n_begin + t * SW;
         const int64_t pn = n0 + p_s;
         const bool pvalid = p_fok && (pn < n_end);
         const int64_t pidx = pn * F + f0 + p_fl;
-        const float v = pvalid ? v_next : 0.0f;
-        v_next = load_x(t + kWaves);
+        const float v = pvalid ? xv : 0.0f;
         const int k = find_bin(v, e_row, p_n);
         const float frac = (v - e_row[k]) * iw_row[k];
         const float qf = quant<Q>(frac);
@@ -330,6 +336,24 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
                                                (n * F + f0 + o_fl) * a.MW, U, lane, o_u, m_shift, m_word);
             }
         }
+    };
+
+    // the early tiles from their registers (shifted down one a tile, so the
+    // loop stays rolled), then the rest with the next tile's x loaded while
+    // the current one is stored
+    const int64_t t_rest = wave + static_cast<int64_t>(kXEarly) * kWaves;
+    float v_next = load_x(t_rest);
+    int64_t t = wave;
+    for (int i = 0; i < kXEarly && t < n_tiles; ++i, t += kWaves) {
+        const float v = x_early[0];
+#pragma unroll
+        for (int j = 0; j + 1 < kXEarly; ++j) x_early[j] = x_early[j + 1];
+        tile(t, v);
+    }
+    for (; t < n_tiles; t += kWaves) {
+        const float v = v_next;
+        v_next = load_x(t + kWaves);
+        tile(t, v);
     }
 }
 
