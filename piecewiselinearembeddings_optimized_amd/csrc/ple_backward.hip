@@ -104,6 +104,11 @@ constexpr int kWideBlock = 2 * kBlock;
 
 constexpr int kBwdRelu = 1;
 constexpr int kBwdLin = 2;
+// (not an epilogue) gradient rows that end inside a 128-byte line: plain
+// loads where the lane group's width would stream them.  Rows of d = 24
+// fp32 (96 bytes): backward 367 -> 304 us at N = 65536, F = 128, 48 bins;
+// d = 32 (whole lines) keeps the streaming loads (286 us; 306 us plain).
+constexpr int kBwdShared = 4;
 
 // finalize (dW / db from the chunk partials): one workgroup per (feature,
 // group of kFinCols columns), kFinLanes lanes per column
@@ -502,13 +507,15 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     constexpr int kGW = grad_words<GD, VEC>();   // dwords of a row per lane (16-bit: two elements each)
     const uint32_t rowFb = static_cast<uint32_t>(F) * D * esz;
     const uint32_t Db = static_cast<uint32_t>(D) * esz;
-    // Gradient rows spanning 128 bytes or more are streamed (non-temporal
-    // loads); narrower rows share lines with a neighbouring feature's rows,
-    // which another run or workgroup reads later, and so do the rows of
-    // 2-float lanes (D = 2 mod 4).  (Fixed per instantiation:
-    // a branch between the two forms around the loads costs more than it
-    // saves.)
-    constexpr int kGCpol = VEC % 4 == 0 && LGW_T * VEC * static_cast<int>(esz) >= 128 ? kCpolNT : 0;
+    // Gradient rows of whole 128-byte lines are streamed (non-temporal
+    // loads); other rows share lines with a neighbouring feature's rows,
+    // which another run or workgroup reads later: narrower lane groups, the
+    // rows of 2-float lanes (D = 2 mod 4), and the twins that the launcher
+    // picks for rows of a lane group's width that end inside a line
+    // (kBwdShared).  (Fixed per instantiation: a branch between the two
+    // forms around the loads costs more than it saves.)
+    constexpr int kGCpol =
+        VEC % 4 == 0 && LGW_T * VEC * static_cast<int>(esz) >= 128 && (EPI & kBwdShared) == 0 ? kCpolNT : 0;
     // idle lanes: an offset past every span
     const uint32_t laneoff = c_ok ? static_cast<uint32_t>(lc) * VEC * esz : 0x80000000u;
     // epilogue inputs of a row (sample s, local feature fl): its mask word
@@ -1447,13 +1454,19 @@ void launch_bwd(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, cons
 template <int GD, int Q, int EPI, int RB>
 hipError_t launch_reduce_epi(const BwdArgs &a, int vec, dim3 grid, size_t lds, hipStream_t s) {
     const dim3 blk(RB);
+    constexpr int esz = GD == PLE_DTYPE_F32 ? 4 : 2;
+    constexpr int SH = EPI | kBwdShared;
+    const bool shared = (static_cast<int64_t>(a.D) * esz) % 128 != 0;   // rows end inside a line
     if (vec == 8) {
         // (16-bit gradients only, D a multiple of 8: groups of 2 to 8 lanes)
         if constexpr (GD != PLE_DTYPE_F32) {
             switch (a.LGW) {
                 case 2: launch_bwd((ple_bwd_fused_kernel<GD, Q, 8, 2, EPI, RB>), grid, blk, lds, s, a); break;
                 case 4: launch_bwd((ple_bwd_fused_kernel<GD, Q, 8, 4, EPI, RB>), grid, blk, lds, s, a); break;
-                default: launch_bwd((ple_bwd_fused_kernel<GD, Q, 8, 8, EPI, RB>), grid, blk, lds, s, a); break;
+                default:
+                    if (shared) launch_bwd((ple_bwd_fused_kernel<GD, Q, 8, 8, SH, RB>), grid, blk, lds, s, a);
+                    else launch_bwd((ple_bwd_fused_kernel<GD, Q, 8, 8, EPI, RB>), grid, blk, lds, s, a);
+                    break;
             }
             return hipGetLastError();
         } else {
@@ -1464,8 +1477,20 @@ hipError_t launch_reduce_epi(const BwdArgs &a, int vec, dim3 grid, size_t lds, h
         switch (a.LGW) {
             case 2: launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 2, EPI, RB>), grid, blk, lds, s, a); break;
             case 4: launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 4, EPI, RB>), grid, blk, lds, s, a); break;
-            case 8: launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 8, EPI, RB>), grid, blk, lds, s, a); break;
-            default: launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 16, EPI, RB>), grid, blk, lds, s, a); break;
+            case 8:
+                // (16-bit rows of 8-lane groups are not streamed: no twin)
+                if constexpr (GD == PLE_DTYPE_F32) {
+                    if (shared) {
+                        launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 8, SH, RB>), grid, blk, lds, s, a);
+                        break;
+                    }
+                }
+                launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 8, EPI, RB>), grid, blk, lds, s, a);
+                break;
+            default:
+                if (shared) launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 16, SH, RB>), grid, blk, lds, s, a);
+                else launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 16, EPI, RB>), grid, blk, lds, s, a);
+                break;
         }
     } else if (vec == 2) {
         // (the planner takes 2 per lane for 6 <= D <= 64: groups of 4 to 32 lanes)

@@ -291,6 +291,8 @@ SHAPES = [
     (700, 3, 30, 38), (400, 3, 15, 62), (500, 2, 20, 47),
     # the forward's 512-thread plans of rows up to 24 columns with up to 8 features a group
     (2048, 128, 48, 24), (2048, 128, 48, 12),
+    # gradient rows ending inside a 128-byte line in lane groups that would stream them (plain-load twins)
+    (1500, 5, 40, 28), (900, 3, 40, 48), (700, 4, 33, 36),
 ]
 
 
@@ -353,6 +355,24 @@ def test_eight_column_lanes_16bit(d, quant, c_oracle, tune):
     gx4, gw4 = ops.backward(g_h.to(DEV), x, e, iw, nb, wt, idx, True, True)
     torch.cuda.synchronize()
     _check_backward(w, quant, g_h.float().numpy(), gx4, gw4, None, c_oracle)
+
+
+@pytest.mark.parametrize("d", [44, 48, 56])
+@pytest.mark.parametrize("quant", ["bf16", "f16"])
+def test_16bit_rows_ending_inside_a_line(d, quant, c_oracle):
+    """16-bit gradient rows of 88, 96 and 112 bytes in lane groups that stream
+    whole-line rows (four columns a lane in 16-lane groups at d = 44, eight
+    columns a lane in 8-lane groups at d = 48 and 56): the launcher's
+    plain-load twins, against the quantisation-aware float64 oracle."""
+    n, f, bmax = 1100, 3, 29
+    w = _random_case(n, f, bmax, d, seed=d + 301)
+    print(f"16-bit rows inside a line {w.name} {quant}", flush=True)
+    x, e, iw, nb, wt, bt = _inputs(w)
+    out, idx = ops.forward(x, e, iw, nb, wt, QUANT_TORCH[quant])
+    g_h = torch.from_numpy(_grad((n, f, d), d + 5)).to(QUANT_TORCH[quant])
+    gx, gw = ops.backward(g_h.to(DEV), x, e, iw, nb, wt, idx, True, True)
+    torch.cuda.synchronize()
+    _check_backward(w, quant, g_h.float().numpy(), gx, gw, None, c_oracle)
 
 
 @pytest.mark.parametrize("d", [10, 30])
