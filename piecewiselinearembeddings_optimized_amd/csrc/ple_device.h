@@ -261,20 +261,24 @@ __device__ __forceinline__ uint32_t pack16(float a, float b) {
 
 // Stores VEC consecutive outputs as OUT (VEC in {1, 2, 4}; 8 for 16-bit OUT).
 // Four or more outputs a lane, and pairs of 16-bit outputs, are stored with
-// the non-temporal hint (the output is written once and not read back here);
-// one or two fp32 outputs and single 16-bit outputs (rows of D not a multiple
-// of 4, resp. odd D) are plain stores, since with the hint they measured up to
-// 40% slower (F=128, 48 bins, N=65536: d=30 fp32 456 -> 321 us, d=31 484 ->
-// 340 us, d=15 bf16 188 -> 165 us without it; pairs of bf16 at d=30 were
-// about even).
-template <int OUT, int VEC>
+// the non-temporal hint when `nt` (the output is written once and not read
+// back here); one or two fp32 outputs and single 16-bit outputs (rows of D not
+// a multiple of 4, resp. odd D) are plain stores, since with the hint they
+// measured up to 40% slower (F=128, 48 bins, N=65536: d=30 fp32 456 -> 321 us,
+// d=31 484 -> 340 us, d=15 bf16 188 -> 165 us without it; pairs of bf16 at
+// d=30 were about even).  NT = false: every store plain.  (A compile-time
+// choice: with a run-time one the compiler merges the two stores into one
+// without the hint.)
+template <int OUT, int VEC, bool NT = true>
 __device__ __forceinline__ void store_out(void *base, int64_t i, const float *v) {
+    constexpr bool nt = NT;
     if constexpr (OUT == PLE_DTYPE_F32) {
         float *p = static_cast<float *>(base) + i;
         if constexpr (VEC == 4) {
             typedef float f32x4 __attribute__((ext_vector_type(4)));
             const f32x4 t = {v[0], v[1], v[2], v[3]};
-            __builtin_nontemporal_store(t, reinterpret_cast<f32x4 *>(p));
+            if constexpr (nt) __builtin_nontemporal_store(t, reinterpret_cast<f32x4 *>(p));
+            else *reinterpret_cast<f32x4 *>(p) = t;
         } else if constexpr (VEC == 2) {
             *reinterpret_cast<float2 *>(p) = make_float2(v[0], v[1]);
         } else {
@@ -286,13 +290,16 @@ __device__ __forceinline__ void store_out(void *base, int64_t i, const float *v)
             typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
             const u32x4 w = {pack16<OUT>(v[0], v[1]), pack16<OUT>(v[2], v[3]), pack16<OUT>(v[4], v[5]),
                              pack16<OUT>(v[6], v[7])};
-            __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(p));
+            if constexpr (nt) __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(p));
+            else *reinterpret_cast<u32x4 *>(p) = w;
         } else if constexpr (VEC == 4) {
             typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
             const u32x2 w = {pack16<OUT>(v[0], v[1]), pack16<OUT>(v[2], v[3])};
-            __builtin_nontemporal_store(w, reinterpret_cast<u32x2 *>(p));
+            if constexpr (nt) __builtin_nontemporal_store(w, reinterpret_cast<u32x2 *>(p));
+            else *reinterpret_cast<u32x2 *>(p) = w;
         } else if constexpr (VEC == 2) {
-            __builtin_nontemporal_store(pack16<OUT>(v[0], v[1]), reinterpret_cast<uint32_t *>(p));
+            if constexpr (nt) __builtin_nontemporal_store(pack16<OUT>(v[0], v[1]), reinterpret_cast<uint32_t *>(p));
+            else *reinterpret_cast<uint32_t *>(p) = pack16<OUT>(v[0], v[1]);
         } else {
             p[0] = OUT == PLE_DTYPE_BF16 ? bf16_bits(v[0]) : f16_bits(v[0]);
         }

@@ -54,6 +54,7 @@ struct FwdArgs {
     int C;        // sample chunks
     int64_t NC;   // samples per chunk
     int FB;       // threads per workgroup (kBlock or 2 * kBlock)
+    int out_nt;   // table kernel: output stores with the non-temporal hint (see forward_run)
     // wide-table kernel: checkpoint stride (bins), LDS offsets (floats) of
     // the weight stage and of the edge / inverse-width tables, and whether
     // the edges and inverse widths are staged in LDS (else read from global)
@@ -89,7 +90,7 @@ __device__ __forceinline__ uint32_t row_or(uint32_t v, int U, int lane, int u) {
 // (this one is lane o_u of them) are gathered into the row's mask words at
 // `mi`.  bvec / lwv: the lane's bias or linear0 weight (linear0 bias in bvec);
 // xs: the sample's x (linear0).
-template <int Q, int OUT, int EPI, int VEC>
+template <int Q, int OUT, int EPI, int VEC, bool NT = true>
 __device__ __forceinline__ void emit_segment(const FwdArgs &a, float (&r)[VEC], const float (&bvec)[VEC],
                                              const float (&lwv)[VEC], float xs, bool row_ok, int64_t oi,
                                              int64_t mi, int U, int lane, int o_u, int m_shift, int m_word) {
@@ -112,7 +113,7 @@ __device__ __forceinline__ void emit_segment(const FwdArgs &a, float (&r)[VEC], 
         if constexpr (LIN) o = fmaf(lwv[t2], xs, bvec[t2]) + o;
         r[t2] = o;
     }
-    if (row_ok) store_out<OUT, VEC>(a.out, oi, r);
+    if (row_ok) store_out<OUT, VEC, NT>(a.out, oi, r);
     if constexpr (RELU) {
         if (a.mask) {
             const uint32_t w0 = row_or(m_word == 0 ? mbits << m_shift : 0u, U, lane, o_u);
@@ -127,8 +128,9 @@ __device__ __forceinline__ void emit_segment(const FwdArgs &a, float (&r)[VEC], 
 }
 
 // FB: threads per workgroup (256, or 512 where the tables leave room for at
-// most two workgroups per CU: twice the waves per staged table)
-template <int Q, int OUT, int EPI, int VEC, typename IdxT, int FB>
+// most two workgroups per CU: twice the waves per staged table); NT: output
+// stores with the non-temporal hint where store_out gives them one
+template <int Q, int OUT, int EPI, int VEC, typename IdxT, int FB, bool NT = true>
 __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
     constexpr int kWaves = FB / kWave;
     // wave tiles whose x is loaded during the table staging: with 512
@@ -331,7 +333,7 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
                     r[0] = fmaf(qs[q], row[D], row[0]);
                 }
                 const bool row_ok = o_ok && s < SW && n < n_end;
-                emit_segment<Q, OUT, EPI, VEC>(a, r, bvec, lwv, LIN ? xs[q] : 0.0f, row_ok,
+                emit_segment<Q, OUT, EPI, VEC, NT>(a, r, bvec, lwv, LIN ? xs[q] : 0.0f, row_ok,
                                                n * row_elems + static_cast<int64_t>(f0 + o_fl) * D + o_u * VEC,
                                                (n * F + f0 + o_fl) * a.MW, U, lane, o_u, m_shift, m_word);
             }
@@ -650,6 +652,20 @@ void launch_fwd(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, cons
     hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), s, t_slot.start, t_slot.stop, 0u, a);
 }
 
+// the table kernel, with plain output stores where the launch asks for them
+// and the instantiation would stream (out_nt)
+template <int Q, int OUT, int EPI, int VEC, typename IdxT, int FB>
+void launch_tbl(const FwdArgs &a, dim3 grid, size_t lds, hipStream_t s) {
+    constexpr bool kHasNT = OUT == PLE_DTYPE_F32 ? VEC >= 4 : VEC >= 2;
+    if constexpr (kHasNT) {
+        if (!a.out_nt) {
+            launch_fwd((ple_fwd_kernel<Q, OUT, EPI, VEC, IdxT, FB, false>), grid, dim3(FB), lds, s, a);
+            return;
+        }
+    }
+    launch_fwd((ple_fwd_kernel<Q, OUT, EPI, VEC, IdxT, FB>), grid, dim3(FB), lds, s, a);
+}
+
 template <int Q, int OUT, int EPI, int VEC>
 hipError_t launch_idx(const FwdArgs &a, int idxb, bool wide, dim3 grid, size_t lds, hipStream_t s) {
     // uint8 indices up to 256 bins, int16 up to 32768, int32 beyond (those
@@ -662,11 +678,11 @@ hipError_t launch_idx(const FwdArgs &a, int idxb, bool wide, dim3 grid, size_t l
     }
     if (idxb == 4) return hipErrorInvalidConfiguration;
     if (a.FB == 2 * kBlock) {
-        if (idxb == 1) launch_fwd((ple_fwd_kernel<Q, OUT, EPI, VEC, uint8_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
-        else launch_fwd((ple_fwd_kernel<Q, OUT, EPI, VEC, int16_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
+        if (idxb == 1) launch_tbl<Q, OUT, EPI, VEC, uint8_t, 2 * kBlock>(a, grid, lds, s);
+        else launch_tbl<Q, OUT, EPI, VEC, int16_t, 2 * kBlock>(a, grid, lds, s);
     } else {
-        if (idxb == 1) launch_fwd((ple_fwd_kernel<Q, OUT, EPI, VEC, uint8_t, kBlock>), grid, dim3(kBlock), lds, s, a);
-        else launch_fwd((ple_fwd_kernel<Q, OUT, EPI, VEC, int16_t, kBlock>), grid, dim3(kBlock), lds, s, a);
+        if (idxb == 1) launch_tbl<Q, OUT, EPI, VEC, uint8_t, kBlock>(a, grid, lds, s);
+        else launch_tbl<Q, OUT, EPI, VEC, int16_t, kBlock>(a, grid, lds, s);
     }
     return hipGetLastError();
 }
@@ -677,11 +693,11 @@ hipError_t launch_vec(const FwdArgs &a, int vec, int idxb, bool wide, dim3 grid,
     if constexpr (OUT != PLE_DTYPE_F32 && EPI == kEpiNone) {
         if (vec == 8 && !wide) {
             if (a.FB == 2 * kBlock) {
-                if (idxb == 1) launch_fwd((ple_fwd_kernel<Q, OUT, EPI, 8, uint8_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
-                else launch_fwd((ple_fwd_kernel<Q, OUT, EPI, 8, int16_t, 2 * kBlock>), grid, dim3(2 * kBlock), lds, s, a);
+                if (idxb == 1) launch_tbl<Q, OUT, EPI, 8, uint8_t, 2 * kBlock>(a, grid, lds, s);
+                else launch_tbl<Q, OUT, EPI, 8, int16_t, 2 * kBlock>(a, grid, lds, s);
             } else {
-                if (idxb == 1) launch_fwd((ple_fwd_kernel<Q, OUT, EPI, 8, uint8_t, kBlock>), grid, dim3(kBlock), lds, s, a);
-                else launch_fwd((ple_fwd_kernel<Q, OUT, EPI, 8, int16_t, kBlock>), grid, dim3(kBlock), lds, s, a);
+                if (idxb == 1) launch_tbl<Q, OUT, EPI, 8, uint8_t, kBlock>(a, grid, lds, s);
+                else launch_tbl<Q, OUT, EPI, 8, int16_t, kBlock>(a, grid, lds, s);
             }
             return hipGetLastError();
         }
@@ -728,6 +744,18 @@ int forward_run(const ForwardRequest &r) {
     a.out = r.out; a.idx = r.idx;
     a.N = r.N; a.F = static_cast<int>(r.F); a.B = static_cast<int>(r.B); a.D = static_cast<int>(r.D);
     a.FS = pl.FS; a.G = pl.G; a.C = pl.C; a.NC = pl.NC; a.FB = pl.FB;
+    // A feature group's outputs of a sample are one segment of FS * D
+    // outputs; the neighbouring group writes the rest of its first and last
+    // lines.  Streaming stores suit segments whose ends fall on 64-byte
+    // boundaries; at other ends the partial writes reach memory unmerged,
+    // and plain stores let the L2 of the XCD, which runs both groups, merge
+    // the lines first (F = 128, 48 bins, N = 65536: d = 28 fp32 380 -> 298 us,
+    // d = 44 504 -> 409 us; at 64-byte ends plain stores lost 15-35%).
+    {
+        const int64_t seg = static_cast<int64_t>(pl.FS) * r.D * out_bytes;
+        const int64_t row = r.F * r.D * out_bytes;
+        a.out_nt = seg % 64 == 0 && row % 64 == 0 && reinterpret_cast<uintptr_t>(r.out) % 64 == 0;
+    }
     a.S = pl.S; a.stage_off = pl.stage_off; a.edge_off = pl.edge_off; a.edges_lds = pl.edges_lds;
     const int64_t grid = kNumXcd * tiles_per_xcd(pl.G, pl.C);
     if (grid > INT32_MAX) return PLE_E_TOO_LARGE;

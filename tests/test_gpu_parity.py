@@ -293,6 +293,8 @@ SHAPES = [
     (2048, 128, 48, 24), (2048, 128, 48, 12),
     # gradient rows ending inside a 128-byte line in lane groups that would stream them (plain-load twins)
     (1500, 5, 40, 28), (900, 3, 40, 48), (700, 4, 33, 36),
+    # forward segments (a feature group's outputs of a sample) ending off 64-byte boundaries: plain stores
+    (800, 6, 30, 44),
 ]
 
 
@@ -363,12 +365,16 @@ def test_16bit_rows_ending_inside_a_line(d, quant, c_oracle):
     """16-bit gradient rows of 88, 96 and 112 bytes in lane groups that stream
     whole-line rows (four columns a lane in 16-lane groups at d = 44, eight
     columns a lane in 8-lane groups at d = 48 and 56): the launcher's
-    plain-load twins, against the quantisation-aware float64 oracle."""
+    plain-load twins, against the quantisation-aware float64 oracle.  The
+    forward's segments end off 64-byte boundaries at d = 44 and 56 (plain
+    stores) and on them at d = 48: bit-exact against the C mirror."""
     n, f, bmax = 1100, 3, 29
     w = _random_case(n, f, bmax, d, seed=d + 301)
     print(f"16-bit rows inside a line {w.name} {quant}", flush=True)
     x, e, iw, nb, wt, bt = _inputs(w)
     out, idx = ops.forward(x, e, iw, nb, wt, QUANT_TORCH[quant])
+    mirror, _ = c_oracle.forward_f32(w.x, w.edges, w.inv_widths, w.n_bins, w.weight, quant=quant)
+    np.testing.assert_array_equal(out.float().cpu().numpy().view(np.uint32), mirror.view(np.uint32))
     g_h = torch.from_numpy(_grad((n, f, d), d + 5)).to(QUANT_TORCH[quant])
     gx, gw = ops.backward(g_h.to(DEV), x, e, iw, nb, wt, idx, True, True)
     torch.cuda.synchronize()
