@@ -119,6 +119,42 @@ constexpr int kFinStride = kFinCols + 1;
 constexpr int kFinLoadsInline = 128;   // chunk-sum loads per finalize thread, at most
 constexpr int kFinLanes = kBlock / kFinCols;   // lanes per column (half a wave)
 
+// One column's dW from its per-bin sums, by kFinLanes lanes (l: this lane's
+// place among them): each lane sums the buckets of its run of the n bins, a
+// suffix scan over the lanes gives every run the sum of the runs above it,
+// and each lane walks its run from the top, dW[phys k] = weighted[k] +
+// sum_{m > k} bucket[m]; slots no bin maps to get 0.  total(k, h): bin k's
+// bucket (h = 0) or weighted (h = 1) sum; dw: the column's dW (stride D
+// between slots) or null.  Returns the lanes' running sums: lane 0 holds the
+// column's bucket total.  Every lane of the group takes part (a lane with
+// n = 0 adds zeros), so the shuffles see live lanes.  A fixed order: results
+// repeat bitwise.
+template <typename Total>
+__device__ __forceinline__ float dw_suffix(Total total, int n, int B, int D, int l, float *dw) {
+    const int m = (n + kFinLanes - 1) / kFinLanes;   // bins per lane
+    const int lo = min(n, l * m);
+    const int hi = min(n, lo + m);
+    float run = 0.0f;
+    for (int k = hi - 1; k >= lo; --k) run += total(k, 0);
+    // inclusive suffix over the lanes: sum of the runs of lanes l, l+1, ...
+    float incl = run;
+#pragma unroll
+    for (int off = 1; off < kFinLanes; off <<= 1) {
+        const float t = __shfl_down(incl, off, kFinLanes);
+        if (l + off < kFinLanes) incl += t;
+    }
+    const float above = __shfl_down(incl, 1, kFinLanes);
+    if (dw) {
+        float fut = l + 1 < kFinLanes ? above : 0.0f;
+        for (int k = hi - 1; k >= lo; --k) {
+            dw[static_cast<int64_t>(phys_bin(k, n, B)) * D] = total(k, 1) + fut;
+            fut += total(k, 0);
+        }
+        for (int k = n - 1 + l; k < B - 1; k += kFinLanes) dw[static_cast<int64_t>(k) * D] = 0.0f;
+    }
+    return incl;
+}
+
 // ---------------------------------------------------------------------------
 // sub-tile sort (all threads of the fused kernel, between reduce phases)
 // ---------------------------------------------------------------------------
@@ -880,13 +916,10 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
 
     // One chunk: this workgroup has seen every sample of its features, so it
     // writes dW and db from the LDS histogram itself, with the finalize
-    // kernel's steps and lane count (the results repeat those of the
-    // two-kernel path bitwise): kFinLanes lanes per column, columns in turn,
-    // each lane sums the buckets of its run of bins, a suffix scan over the
-    // lanes gives every run the sum of the runs above it, and each lane walks
-    // its run from the top, dW[phys k] = weighted[k] + sum_{m > k} bucket[m];
-    // slots no bin maps to get 0.  Whole lane groups run every pass (a group
-    // past the live columns scans zeros), so the shuffles see live lanes.
+    // kernel's steps and lane count (dw_suffix; the results repeat those of
+    // the two-kernel path bitwise), kFinLanes lanes per column, columns in
+    // turn.  Whole lane groups run every pass (a group past the live columns
+    // scans zeros).
     if (a.fin_fused) {
         constexpr int kGroups = NTH / kFinLanes;
         const int l = tid % kFinLanes;
@@ -898,29 +931,10 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
             const int j = ok ? col - fl * D : 0;
             const int n = ok ? s_nb[fl] : 0;
             const float *h = s_hist + static_cast<size_t>(fl) * B * D2 + j;   // bucket at k * D2, weighted at + D
-            const int m = (n + kFinLanes - 1) / kFinLanes;
-            const int lo = min(n, l * m);
-            const int hi = min(n, lo + m);
-            float run = 0.0f;
-            for (int k = hi - 1; k >= lo; --k) run += h[k * D2];
-            float incl = run;
-#pragma unroll
-            for (int off = 1; off < kFinLanes; off <<= 1) {
-                const float t = __shfl_down(incl, off, kFinLanes);
-                if (l + off < kFinLanes) incl += t;
-            }
-            const float above = __shfl_down(incl, 1, kFinLanes);
-            if (!ok) continue;
-            const int64_t wrow = static_cast<int64_t>(f0 + fl) * B;
-            if (a.dw) {
-                float fut = l + 1 < kFinLanes ? above : 0.0f;
-                for (int k = hi - 1; k >= lo; --k) {
-                    a.dw[(wrow + phys_bin(k, n, B)) * D + j] = h[k * D2 + D] + fut;
-                    fut += h[k * D2];
-                }
-                for (int k = n - 1 + l; k < B - 1; k += kFinLanes) a.dw[(wrow + k) * D + j] = 0.0f;
-            }
-            if (l == 0) {
+            auto total = [&](int k, int hh) __attribute__((always_inline)) { return h[k * D2 + hh * D]; };
+            float *dwc = ok && a.dw ? a.dw + static_cast<int64_t>(f0 + fl) * B * D + j : nullptr;
+            const float incl = dw_suffix(total, n, B, D, l, dwc);
+            if (ok && l == 0) {
                 const int64_t fj = static_cast<int64_t>(f0 + fl) * D + j;
                 if (a.db) a.db[fj] = a.db_from_buckets ? incl : s_db[fl * D + j];
                 if constexpr (kLin) {
@@ -1123,12 +1137,9 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_chunksum_kernel(float *part, i
 // Sums the chunk partials of every (bin, column) of the group in chunk order
 // into LDS (or reads their sums from chunk 0, where ple_bwd_chunksum_kernel
 // left them: many bins or chunks), then kFinLanes lanes per column take the
-// suffix over logical
-// bins, dW[phys(k)] = weighted[k] + sum_{m>k} bucket[m]: each lane sums the
-// buckets of its run of bins, a suffix scan over the lanes gives every run the
-// sum above it, and each lane walks its run from the top.  Slots no bin maps
-// to get 0.  The bias gradient is the sum of all buckets (fp32 gradients) or
-// its own summed partials.  A fixed order throughout: results repeat bitwise.
+// suffix over logical bins (dw_suffix).  The bias gradient is the sum of all
+// buckets (fp32 gradients) or its own summed partials.  A fixed order
+// throughout: results repeat bitwise.
 
 __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
     extern __shared__ float tot[];       // [n][2][kFinStride]
@@ -1172,27 +1183,7 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
     const int64_t wrow = static_cast<int64_t>(f) * B;
     const bool sum_buckets = a.dw || (a.db && a.db_from_buckets);
     if (sum_buckets) {
-        const int m = (n + kFinLanes - 1) / kFinLanes;   // bins per lane
-        const int lo = min(n, l * m);
-        const int hi = min(n, lo + m);
-        float run = 0.0f;
-        for (int k = hi - 1; k >= lo; --k) run += total(k, 0);
-        // inclusive suffix over the lanes: sum of the runs of lanes l, l+1, ...
-        float incl = run;
-#pragma unroll
-        for (int off = 1; off < kFinLanes; off <<= 1) {
-            const float t = __shfl_down(incl, off, kFinLanes);
-            if (l + off < kFinLanes) incl += t;
-        }
-        const float above = __shfl_down(incl, 1, kFinLanes);
-        if (a.dw) {
-            float fut = l + 1 < kFinLanes ? above : 0.0f;
-            for (int k = hi - 1; k >= lo; --k) {
-                a.dw[(wrow + phys_bin(k, n, B)) * D + j] = total(k, 1) + fut;
-                fut += total(k, 0);
-            }
-            for (int k = n - 1 + l; k < B - 1; k += kFinLanes) a.dw[(wrow + k) * D + j] = 0.0f;
-        }
+        const float incl = dw_suffix(total, n, B, D, l, a.dw ? a.dw + wrow * D + j : nullptr);
         if (a.db && a.db_from_buckets && l == 0) a.db[static_cast<int64_t>(f) * D + j] = incl;
     }
     if (l == 0) {
