@@ -60,12 +60,14 @@ def _parse():
 
 
 def _traffic(kernel: str, workload: str):
-    """HBM bytes per launch measured by rocprofv3 PMC runs, if committed."""
+    """HBM bytes per launch measured by rocprofv3 PMC runs, if committed, and
+    the commit of the build they measured."""
     path = os.path.join(REPO, "profiles", f"traffic_{kernel}_{workload}.json")
     if not os.path.exists(path):
-        return None
+        return None, None
     with open(path) as fh:
-        return json.load(fh).get("bytes_per_launch")
+        rec = json.load(fh)
+    return rec.get("bytes_per_launch"), rec.get("measured_commit")
 
 
 # dense [rows, F, Bmax] elements the CPU baseline's sample may hold (c1 in full:
@@ -341,6 +343,25 @@ def main():
 
     fwd_op_ms, fwd_op_med = time_pass(fwd, args.steps)
     _, idx = fwd()
+
+    def peak_bytes(fn):
+        """Device memory a call allocates at its peak beyond what is held
+        before it (the reference benchmark's incremental peak,
+        tests/test_ple_cuda_benchmark.py:935-971)."""
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        res = fn()
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated()
+        del res
+        return max(0, peak - base)
+
+    memory = {"fwd_peak_bytes": peak_bytes(fwd)}
+    if args.mode == "fwdbwd":
+        memory["bwd_peak_bytes"] = peak_bytes(lambda: bwd(idx))
+        memory["step_peak_bytes"] = peak_bytes(lambda: bwd(fwd()[1]))
+        memory["bwd_workspace_bytes"] = capi.workspace_bytes(n, f, bmax, d)
     bwd_op_ms = bwd_op_med = 0.0
     if args.mode == "fwdbwd":
         bwd_op_ms, bwd_op_med = time_pass(lambda: bwd(idx), args.steps)
@@ -357,11 +378,17 @@ def main():
     median_ms = 0.5 * (reps[4] + reps[5])
 
     fwd_bytes, bwd_bytes = workloads.algorithmic_bytes(n, f, bmax, d, out_bytes=out_bytes)
-    # the backward's gradient kernel writes no dW / db (its finalize does)
-    bwd_kernel_bytes = bwd_bytes - f * bmax * d * 4 - f * d * 4
+    # The backward's plan decides what its timed kernel writes: with one chunk
+    # the sorted path's gradient kernel writes dW / db itself, otherwise a
+    # finalize kernel does (from chunk partials).  The fallback path's timer
+    # spans its dx and histogram kernels.
+    plan = capi.backward_plan(n, f, bmax, d, grad_dtype=g.dtype, quant_dtype=quant, grad_output=g)
+    bwd_kernel_bytes = bwd_bytes
+    if not (plan["sorted"] and plan["chunks"] == 1):
+        bwd_kernel_bytes -= f * bmax * d * 4 + f * d * 4
     kernels = {}
     fwd_name = "ple_fwd_kernel"
-    bwd_name = "ple_bwd_fused_kernel"
+    bwd_name = "ple_bwd_fused_kernel" if plan["sorted"] else "ple_bwd_simple_dx_kernel+ple_bwd_simple_hist_kernel"
     for name, key, nbytes in ((fwd_name, "fwd", fwd_bytes), (bwd_name, "bwd", bwd_kernel_bytes)):
         total_ms, launches = kern[key]
         if launches == 0:
@@ -372,6 +399,7 @@ def main():
                          "frac": nbytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
     dom_name = max(kernels, key=lambda k: kernels[k]["ms"])
     dom = kernels[dom_name]
+    traffic, traffic_commit = _traffic(dom_name, w.name)
     total_bytes = fwd_bytes + (bwd_bytes if args.mode == "fwdbwd" else 0)
 
     cpu = None
@@ -410,6 +438,8 @@ def main():
         "bwd_op_ms": bwd_op_ms,
         "bwd_op_median_ms": bwd_op_med,
         "kernels": kernels,
+        "memory": memory,
+        "backward_plan": plan,
         "roofline": {
             "kernel": dom_name,
             "bound": "hbm",
@@ -417,7 +447,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": dom["frac"],
-            "traffic": _traffic(dom_name, w.name),
+            "traffic": traffic,
+            "traffic_measured_commit": traffic_commit,
             "algorithmic_bytes": dom["bytes"],
             "ms": dom["ms"],
         },

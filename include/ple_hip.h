@@ -86,11 +86,13 @@ int ple_bin_index_bytes(int64_t max_n_bins);
  * Supported pairings: output_dtype == quant_dtype with bias NULL (the
  * reference operator), or output_dtype == PLE_DTYPE_F32 with a bias (the
  * module's "x_ple + bias" fused into the store); others -> PLE_E_UNSUPPORTED.
- * N may be 0 (no launch).  F, B, D >= 1; D <= 64 (the reference module's
- * limit); B <= 2^24 and F * B * D < 2^30 (else PLE_E_TOO_LARGE).  Every such
- * shape runs: per-feature tables that fit LDS take the table kernel, larger
- * ones (many bins times a wide row) a kernel that keeps prefix checkpoints in
- * LDS and reads the weights from global memory -- bit-identical results.
+ * N may be 0 (no launch).  F, B, D >= 1, any D (as the reference operator,
+ * csrc/forward_cuda.cu:764-766: only the reference module asserts D <= 64);
+ * B <= 2^24 and F * B * D < 2^30 (else PLE_E_TOO_LARGE).  Every such shape
+ * runs: per-feature tables that fit LDS take the table kernel, larger ones
+ * (many bins times a wide row) a kernel that keeps prefix checkpoints in LDS
+ * and reads the weights from global memory -- bit-identical results; rows of
+ * more than 64 lanes' columns are split into column chunks.
  */
 int ple_forward_launch(const float *x, const float *bin_edges, const float *inv_bin_widths,
                        const int32_t *n_bins, const float *weight, const float *bias,
@@ -146,6 +148,41 @@ int ple_backward_launch_noalloc(const void *grad_output, const float *x, const f
                                 const void *bin_indices, float *grad_x, float *grad_weight, float *grad_bias,
                                 int64_t N, int64_t F, int64_t B, int64_t D, int grad_dtype, int quant_dtype,
                                 void *stream);
+
+/*
+ * The backward's launch plan for a shape, for benchmarks and memory
+ * accounting; no counterpart in the reference (its launcher picks private,
+ * sorted or atomic dW paths internally, csrc/backward_cuda.cu:1141-1463, and
+ * reports nothing).  grad_output: the gradient that will be passed (its
+ * alignment picks the lane width; NULL = 16-byte aligned); relu / linear0:
+ * the module epilogue of ple_backward_epilogue_launch (0 for
+ * ple_backward_launch).  Fills *info; returns PLE_OK or PLE_E_*.
+ *   sorted             1: the fused sort + reduce + dx kernel; 0: the
+ *                      fallback dx and histogram kernels
+ *   chunks             sample chunks with dW / db partials in the workspace
+ *                      (sorted path with 1 chunk: the gradient kernel writes
+ *                      grad_weight / grad_bias itself, no finalize kernel)
+ *   features_per_group features per gradient-kernel workgroup (sorted path)
+ *   columns_per_lane   gradient elements a lane holds per row (sorted path)
+ *   lanes_per_row      lanes that share a row (sorted path)
+ *   threads            gradient-kernel workgroup size
+ *   lds_bytes          gradient-kernel LDS per workgroup
+ *   workspace_bytes    workspace a launch that writes grad_weight / grad_bias
+ *                      needs (0 for grad_x alone)
+ */
+typedef struct ple_backward_plan_info {
+    int sorted;
+    int chunks;
+    int features_per_group;
+    int columns_per_lane;
+    int lanes_per_row;
+    int threads;
+    size_t lds_bytes;
+    size_t workspace_bytes;
+} ple_backward_plan_info_t;
+int ple_backward_plan_query(const void *grad_output, int64_t N, int64_t F, int64_t B, int64_t D,
+                            int grad_dtype, int quant_dtype, int relu, int linear0,
+                            ple_backward_plan_info_t *info);
 
 /*
  * Module epilogue fused into the kernels.  No counterpart in the reference's

@@ -43,6 +43,21 @@ class Epilogue(ctypes.Structure):
     ]
 
 
+class BackwardPlanInfo(ctypes.Structure):
+    """``ple_backward_plan_info_t``: the backward's launch plan for a shape."""
+
+    _fields_ = [
+        ("sorted", ctypes.c_int),
+        ("chunks", ctypes.c_int),
+        ("features_per_group", ctypes.c_int),
+        ("columns_per_lane", ctypes.c_int),
+        ("lanes_per_row", ctypes.c_int),
+        ("threads", ctypes.c_int),
+        ("lds_bytes", ctypes.c_size_t),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class PleError(RuntimeError):
     def __init__(self, code: int, message: str):
         super().__init__(f"{message} (code {code})")
@@ -69,6 +84,9 @@ def lib() -> ctypes.CDLL:
         L.ple_backward_launch.restype = i32
         L.ple_backward_launch_noalloc.argtypes = [p, p, p, p, p, p, p, p, p, p, i64, i64, i64, i64, i32, i32, p]
         L.ple_backward_launch_noalloc.restype = i32
+        L.ple_backward_plan_query.argtypes = [p, i64, i64, i64, i64, i32, i32, i32, i32,
+                                              ctypes.POINTER(BackwardPlanInfo)]
+        L.ple_backward_plan_query.restype = i32
         ep = ctypes.POINTER(Epilogue)
         L.ple_forward_epilogue_launch.argtypes = [p, p, p, p, p, ep, p, p, i64, i64, i64, i64, i32, p]
         L.ple_forward_epilogue_launch.restype = i32
@@ -146,6 +164,17 @@ def forward(x, bin_edges, inv_bin_widths, n_bins, weight, bias, output, bin_indi
 
 def workspace_bytes(n: int, f: int, bmax: int, d: int) -> int:
     return int(lib().ple_backward_workspace_bytes(n, f, bmax, d))
+
+
+def backward_plan(n: int, f: int, bmax: int, d: int, grad_dtype=torch.float32, quant_dtype=None,
+                  relu: bool = False, linear0: bool = False, grad_output=None) -> dict:
+    """``ple_backward_plan_query``: the plan a backward launch of this shape
+    takes, as a dict of :class:`BackwardPlanInfo`'s fields."""
+    info = BackwardPlanInfo()
+    q = grad_dtype if quant_dtype is None else quant_dtype
+    check(lib().ple_backward_plan_query(_ptr(grad_output), n, f, bmax, d, dtype_code(grad_dtype), dtype_code(q),
+                                        1 if relu else 0, 1 if linear0 else 0, ctypes.byref(info)))
+    return {name: getattr(info, name) for name, _ in BackwardPlanInfo._fields_}
 
 
 def backward(grad_output, x, bin_edges, inv_bin_widths, n_bins, weight, bin_indices, grad_x, grad_weight,

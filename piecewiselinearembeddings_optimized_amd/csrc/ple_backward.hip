@@ -373,7 +373,7 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     constexpr bool kRawDb = !kGradExact || kLin;
     extern __shared__ __align__(16) unsigned char lds[];
     const int FS = a.FS, B = a.B, D = a.D, F = a.F, NT = a.NT;
-    float *s_qw = reinterpret_cast<float *>(lds + a.ro_qw);             // [FS][B][D]
+    float *s_qw = reinterpret_cast<float *>(lds + a.ro_qw);             // [FS][B][D] q(W) * iw
     float *s_hist = reinterpret_cast<float *>(lds + a.ro_hist);         // [FS][B][2D]
     float *s_db = reinterpret_cast<float *>(lds + a.ro_db);             // [FS][D]
     float *s_iw = reinterpret_cast<float *>(lds + a.ro_iw);             // [FS][B]
@@ -437,6 +437,8 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         }
     }
     __syncthreads();
+    // the weight rows pre-scaled by their bin's inverse width: a row's dx term
+    // iw_k <g, q(W[phys k])> is then one dot product with the table row
     for (int i = tid; i < FS * B * D; i += NTH) {
         const int fl = i / (B * D);
         const int r = i - fl * (B * D);
@@ -445,7 +447,9 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         float w = 0.0f;
         if (fl < nfh) {
             const int n = s_nb[fl];
-            if (k < n) w = quant<Q>(a.weight[(static_cast<int64_t>(f0 + fl) * B + phys_bin(k, n, B)) * D + j]);
+            if (k < n)
+                w = quant<Q>(a.weight[(static_cast<int64_t>(f0 + fl) * B + phys_bin(k, n, B)) * D + j]) *
+                    s_iw[fl * B + k];
         }
         s_qw[i] = w;
     }
@@ -480,58 +484,16 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         return static_cast<int>(((y & 0xffffff) << fs_shift) + (y >> 24));
     };
 
-    // F-phase state of a run: running sums of its current key (feature,
-    // bin) -- packed as fl << 12 | k -- and, with rounding quantisation, of
-    // its feature.  Rows past a piece's end and idle lanes (lc >= D / VEC)
-    // load from past the end of the gradient buffer, which reads zeros: they
-    // add nothing and need no masking.
-    int cur = -1, db_fl = -1;
-    bool first_key = true, first_fl = true;
-    float ab[VEC], aw[VEC], ad[VEC], ax[VEC];
+    // F-phase state of a run: the key (feature, bin) of its first piece --
+    // packed as fl << 12 | k, -1 for an empty run -- and that key's feature.
+    // Each piece's sums go straight to LDS: those of the run's first key into
+    // the run's record, every other key into the histogram (the run is that
+    // key's only writer in this sub-tile), and likewise for the per-feature
+    // sums.  Rows past a piece's end and idle lanes (lc >= D / VEC) load from
+    // past the end of the gradient buffer, which reads zeros: they add
+    // nothing and need no masking.
+    int key0 = -1, fl0 = -1;
     float *rec = s_rec + lg * RS + lc * VEC;
-
-    // first key of the run -> record; later keys -> straight into the
-    // histogram (this run is their only writer).  One read-modify-write
-    // through a selected pointer keeps the code inlined per piece small.
-    auto flush_key = [&]() __attribute__((always_inline)) {
-        if (cur < 0) return;
-        float *h = s_hist + __umul24(__umul24(cur >> 12, B) + (cur & 0xfff), D2) + lc * VEC;
-        float *dst = first_key ? rec : h;
-        if (c_ok) {
-            float ob[VEC], ow[VEC];
-            lds_load_vec<VEC>(dst, ob);
-            lds_load_vec<VEC>(dst + D, ow);
-#pragma unroll
-            for (int q = 0; q < VEC; ++q) {
-                ob[q] = first_key ? ab[q] : ob[q] + ab[q];
-                ow[q] = first_key ? aw[q] : ow[q] + aw[q];
-            }
-            lds_store_vec<VEC>(dst, ob);
-            lds_store_vec<VEC>(dst + D, ow);
-        }
-        if (first_key && lc == 0) s_rkey[lg] = cur;
-        first_key = false;
-    };
-    auto flush_fl = [&]() __attribute__((always_inline)) {
-        if (db_fl < 0) return;
-        float *dst = first_fl ? rec + D2 : s_db + db_fl * D + lc * VEC;
-        if (c_ok) {
-            float o[VEC];
-            lds_load_vec<VEC>(dst, o);
-#pragma unroll
-            for (int q = 0; q < VEC; ++q) o[q] = first_fl ? ad[q] : o[q] + ad[q];
-            lds_store_vec<VEC>(dst, o);
-            if constexpr (kLin) {
-                float *dx2 = first_fl ? rec + D2 + D : s_dlw + db_fl * D + lc * VEC;
-                lds_load_vec<VEC>(dx2, o);
-#pragma unroll
-                for (int q = 0; q < VEC; ++q) o[q] = first_fl ? ax[q] : o[q] + ax[q];
-                lds_store_vec<VEC>(dx2, o);
-            }
-        }
-        if (first_fl && lc == 0) s_rfl[lg] = db_fl;   // (kRawDb only)
-        first_fl = false;
-    };
 
     // The current sub-tile: its descriptor and piece buffers, lane group
     // lg's run of contiguous pieces [j0, j1) (m pieces per run, the same for
@@ -585,6 +547,8 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         m = (NPc + LG - 1) / LG;
         j0 = lg * m;
         j1 = min(j0 + m, NPc);
+        key0 = j0 < j1 ? static_cast<int>(t_piece[j0] & 0xffff) : -1;
+        fl0 = key0 >> 12;
         sub = static_cast<int64_t>(t) * NT;
         ns = static_cast<int>(min(static_cast<int64_t>(NT), a.N - sub));
         const int64_t row0 = sub * F + f0;
@@ -638,41 +602,36 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         }
     };
 
-    // weight rows k and k-1 and their inverse widths for the current
-    // key, reloaded from LDS when the key changes (idle lanes read
-    // column 0; their g is 0); row k-1 serves rows with x on e_k
-    float wk[VEC], wp[VEC], lw[VEC];
-    float iwk = 0.0f, iwp = 0.0f;
-#pragma unroll
-    for (int q = 0; q < VEC; ++q) wk[q] = wp[q] = lw[q] = 0.0f;
+    // Per piece: its key's row of the pre-scaled weight table (idle lanes
+    // read column 0; their g is 0), the piece's sums in registers, then
+    // added to LDS (the run's record or the histogram) before the next piece.
+    // Row k-1 of the table serves rows with x on e_k (loaded only for them).
     auto process = [&](int tt, const uint32_t (&gv)[kL][kGW], const uint2 (&dsc)[kL], uint32_t pe,
                        const uint32_t (&mv)[kL], const float (&xv)[kL]) __attribute__((always_inline)) {
         const bool real = j0 + tt < j1;
         const int n = real ? static_cast<int>(pe >> 28) + 1 : 0;
-        const int key = real ? static_cast<int>(pe & 0xffff) : cur;
+        // (an empty piece past the run's end carries some piece's entry:
+        // its table reads stay in range and it adds nothing)
+        const int key = static_cast<int>(pe & 0xffff);
         const int fl = key >> 12;
-        if (key != cur) {
-            flush_key();
-#pragma unroll
-            for (int q = 0; q < VEC; ++q) ab[q] = aw[q] = 0.0f;
-            if constexpr (kRawDb) {
-                if (fl != db_fl) {
-                    flush_fl();
-#pragma unroll
-                    for (int q = 0; q < VEC; ++q) ad[q] = ax[q] = 0.0f;
-                    db_fl = fl;
-                }
-            }
-            if constexpr (kLin) lds_load_vec<VEC>(s_lw + __umul24(fl, D) + lcx * VEC, lw);
-            cur = key;
-            const int k = key & 0xfff;
-            const int kp = k > 0 ? k - 1 : 0;
-            const int rowbase = __umul24(fl, B);
-            lds_load_vec<VEC>(s_qw + __umul24(rowbase + k, D) + lcx * VEC, wk);
-            lds_load_vec<VEC>(s_qw + __umul24(rowbase + kp, D) + lcx * VEC, wp);
-            iwk = s_iw[rowbase + k];
-            iwp = s_iw[rowbase + kp];
-        }
+        const int k = key & 0xfff;
+        const int rowbase = __umul24(fl, B);
+        float wk[VEC], lw[VEC], wp[VEC];
+        lds_load_vec<VEC>(s_qw + __umul24(rowbase + k, D) + lcx * VEC, wk);
+        if constexpr (kLin) lds_load_vec<VEC>(s_lw + __umul24(fl, D) + lcx * VEC, lw);
+        float ab[VEC], aw[VEC], ad[VEC], ax[VEC];
+        // The piece's sums are added into LDS (a read-modify-write: this
+        // lane group owns the cells): the run's first key (feature) into its
+        // record, any other key (feature) into the histogram (bias sums).
+        // The reads are issued here, ahead of the arithmetic; LDS keeps a
+        // wave's accesses in order, so they see the previous piece's writes.
+        // (Reads are harmless for idle lanes and empty pieces; only their
+        // writes are skipped.)
+        const bool add_ok = n > 0 && c_ok;
+        float *dst = key == key0 ? rec : s_hist + __umul24(rowbase + k, D2) + lc * VEC;
+        float hb[VEC], hw[VEC];
+        lds_load_vec<VEC>(dst, hb);
+        lds_load_vec<VEC>(dst + D, hw);
         // g of row i, column q of this lane: masked by the forward's ReLU
         // pass bit, rounded through Q
         auto g_masked = [&](int i, int q, uint32_t mvi) __attribute__((always_inline)) {
@@ -691,6 +650,7 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         // epilogues' kernels fold it into the first pass (a second pass
         // there takes them past 256 VGPRs, one wave per SIMD).
         constexpr bool kEdgePass = !kRelu && !kLin;
+        if constexpr (!kEdgePass) lds_load_vec<VEC>(s_qw + __umul24(rowbase + (k > 0 ? k - 1 : 0), D) + lcx * VEC, wp);
         float parts[kL];
         bool edge = false;
 #pragma unroll
@@ -704,28 +664,33 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
             for (int q = 0; q < VEC; ++q) {
                 const float gm = g_masked(i, q, mvi);
                 const float gq = kGradExact ? gm : quant<Q>(gm);
-                ab[q] += gq;
-                aw[q] = fmaf(qf, gq, aw[q]);
-                if constexpr (kRawDb) ad[q] += kLin ? grad_elem<GD>(gv[i], q) : gm;
+                // (the first row starts the piece's sums)
+                ab[q] = i == 0 ? gq : ab[q] + gq;
+                aw[q] = i == 0 ? qf * gq : fmaf(qf, gq, aw[q]);
+                if constexpr (kRawDb) {
+                    const float gd = kLin ? grad_elem<GD>(gv[i], q) : gm;
+                    ad[q] = i == 0 ? gd : ad[q] + gd;
+                }
                 if constexpr (kLin) {
                     const float graw = grad_elem<GD>(gv[i], q);
-                    ax[q] = fmaf(graw, xvi, ax[q]);
+                    ax[q] = i == 0 ? graw * xvi : fmaf(graw, xvi, ax[q]);
                     dotl = fmaf(graw, lw[q], dotl);
                 }
                 dot = fmaf(gq, wk[q], dot);
                 if constexpr (!kEdgePass) dot2 = fmaf(gq, wp[q], dot2);
             }
-            float part = dot * iwk;
+            float part = dot;
             if constexpr (kLin) part += dotl;
             // x on the bin's left edge (k >= 1, marked by q(frac) = -0): the
             // lower bin's term too
-            if constexpr (!kEdgePass) part = dsc[i].x == 0x80000000u ? fmaf(dot2, iwp, part) : part;
+            if constexpr (!kEdgePass) part = dsc[i].x == 0x80000000u ? part + dot2 : part;
             parts[i] = part;
             edge = edge || dsc[i].x == 0x80000000u;
         }
         // Edge rows are rare in most data: the wave takes this branch only
         // when one of its lane groups holds one.
         if (kEdgePass && __any(edge)) {
+            lds_load_vec<VEC>(s_qw + __umul24(rowbase + (k > 0 ? k - 1 : 0), D) + lcx * VEC, wp);
 #pragma unroll
             for (int i = 0; i < kL; ++i) {
                 const uint32_t mvi = mask_word(i);
@@ -735,7 +700,35 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
                     const float gm = g_masked(i, q, mvi);
                     dot2 = fmaf(kGradExact ? gm : quant<Q>(gm), wp[q], dot2);
                 }
-                if (dsc[i].x == 0x80000000u) parts[i] = fmaf(dot2, iwp, parts[i]);
+                if (dsc[i].x == 0x80000000u) parts[i] += dot2;
+            }
+        }
+        if (add_ok) {
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) {
+                hb[q] += ab[q];
+                hw[q] += aw[q];
+            }
+            lds_store_vec<VEC>(dst, hb);
+            lds_store_vec<VEC>(dst + D, hw);
+            if constexpr (kRawDb) {
+                // (the per-feature sums of the epilogue kernels: read here,
+                // not ahead, to keep their registers down)
+                const bool first = fl == fl0;
+                float *dstd = first ? rec + D2 : s_db + __umul24(fl, D) + lc * VEC;
+                float hd[VEC];
+                lds_load_vec<VEC>(dstd, hd);
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) hd[q] += ad[q];
+                lds_store_vec<VEC>(dstd, hd);
+                if constexpr (kLin) {
+                    float *dstx = first ? rec + D2 + D : s_dlw + __umul24(fl, D) + lc * VEC;
+                    float hx[VEC];
+                    lds_load_vec<VEC>(dstx, hx);
+#pragma unroll
+                    for (int q = 0; q < VEC; ++q) hx[q] += ax[q];
+                    lds_store_vec<VEC>(dstx, hx);
+                }
             }
         }
         // dx into the rows' descriptors (rows past the piece's end: the
@@ -807,14 +800,17 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
 
         // F. pieces: lane group lg takes the contiguous pieces [j0, j1) (its
         //    "run"); piece 0 is in flight already
-        cur = -1;
-        db_fl = -1;
-        first_key = first_fl = true;
+        // the run's record starts at zero (its reads by the previous
+        // sub-tile's merge finished before the sort's barriers)
+        if (c_ok) {
+            float z[VEC];
 #pragma unroll
-        for (int q = 0; q < VEC; ++q) ab[q] = aw[q] = ad[q] = ax[q] = 0.0f;
+            for (int q = 0; q < VEC; ++q) z[q] = 0.0f;
+            for (int h = 0; h < RS; h += D) lds_store_vec<VEC>(rec + h, z);
+        }
         if (lc == 0) {
-            s_rkey[lg] = -1;
-            if constexpr (kRawDb) s_rfl[lg] = -1;
+            s_rkey[lg] = key0;
+            if constexpr (kRawDb) s_rfl[lg] = fl0;
         }
         if (m > 0) {
             int tt = 0;
@@ -830,8 +826,6 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
             if (tt < m) process(tt, gA, dA, pA, mA, xA);
             if (tt + 1 < m) process(tt + 1, gB, dB, pB, mB, xB);
         }
-        flush_key();
-        if constexpr (kRawDb) flush_fl();
         __syncthreads();
         const int64_t h_sub = sub;
         const int h_ns = ns;
@@ -1013,26 +1007,30 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_simple_dx_kernel(BwdArgs a) {
     }
 }
 
-// One wave per (feature, sample chunk); lane j owns column j (D <= 64) and
-// walks the chunk in sample order, folding runs of equal bins into its own
-// cells: in LDS ({bucket} [B][D] then {weighted} [B][D]), copied to the
-// chunk's partials at the end, or -- GLOBAL, tables beyond LDS -- straight in
-// the chunk's partials [B][2D] in global memory, which only this lane reads
-// and writes.  Either way one fixed order per cell.
+// One wave per (feature, sample chunk, block of 64 columns); lane jj owns
+// column j = 64 * block + jj and walks the chunk in sample order, folding
+// runs of equal bins into its own cells: in LDS ({bucket} [B][W] then
+// {weighted} [B][W], W = the block's columns), copied to the chunk's partials
+// at the end, or -- GLOBAL, tables beyond LDS -- straight in the chunk's
+// partials [B][2D] in global memory, which only this lane reads and writes.
+// Either way one fixed order per cell.
 template <int GD, int Q, typename IdxT, bool GLOBAL>
 __global__ __launch_bounds__(kWave) void ple_bwd_simple_hist_kernel(BwdArgs a) {
     extern __shared__ float smem[];
     const int B = a.B, D = a.D, F = a.F;
     const int f = blockIdx.x % F;
-    const int c = blockIdx.x / F;
-    const int j = threadIdx.x;
-    const bool jok = j < D;
+    const int c = (blockIdx.x / F) % a.C;
+    const int jb = blockIdx.x / (F * a.C) * kWave;     // the block's first column
+    const int W = min(kWave, D - jb);                  // its columns
+    const int jj = threadIdx.x;
+    const int j = jb + jj;
+    const bool jok = jj < W;
     const int n_real = clamp_nbins(a.nbins[f], B);
     float *dst = a.part + (static_cast<int64_t>(c) * F + f) * B * 2 * D;
     // bucket / weighted cell of bin k for this lane's column
-    float *hb = GLOBAL ? dst + j : smem + j;
-    float *hw = GLOBAL ? dst + D + j : smem + static_cast<int64_t>(B) * D + j;
-    const int cstride = GLOBAL ? 2 * D : D;
+    float *hb = GLOBAL ? dst + j : smem + jj;
+    float *hw = GLOBAL ? dst + D + j : smem + static_cast<int64_t>(B) * W + jj;
+    const int cstride = GLOBAL ? 2 * D : W;
     if (jok) {
         for (int k = 0; k < n_real; ++k) {
             hb[static_cast<int64_t>(k) * cstride] = 0.0f;
@@ -1093,11 +1091,11 @@ __global__ __launch_bounds__(kWave) void ple_bwd_simple_hist_kernel(BwdArgs a) {
     }
     if constexpr (!GLOBAL) {
         __syncthreads();
-        for (int i = j; i < n_real * D; i += kWave) {
-            const int k = i / D;
-            const int jj = i - k * D;
-            dst[static_cast<int64_t>(k) * 2 * D + jj] = smem[i];
-            dst[static_cast<int64_t>(k) * 2 * D + D + jj] = smem[static_cast<int64_t>(B) * D + i];
+        for (int i = jj; i < n_real * W; i += kWave) {
+            const int k = i / W;
+            const int col = jb + (i - k * W);
+            dst[static_cast<int64_t>(k) * 2 * D + col] = smem[i];
+            dst[static_cast<int64_t>(k) * 2 * D + D + col] = smem[static_cast<int64_t>(B) * W + i];
         }
     }
     if (jok) a.part_db[(static_cast<int64_t>(c) * F + f) * D + j] = cdb;
@@ -1389,14 +1387,19 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
         if (c < 1) c = 1;
         pl.NC = (N + c - 1) / c;
         pl.C = pl.Cd = static_cast<int>((N + pl.NC - 1) / pl.NC);
-        // histogram cells in LDS when they fit, else in the partials themselves
-        pl.lds = static_cast<size_t>(B) * D * 2 * sizeof(float);
+        // histogram cells (of one block of up to 64 columns) in LDS when they
+        // fit, else in the partials themselves
+        pl.lds = static_cast<size_t>(B) * std::min<int64_t>(D, kWave) * 2 * sizeof(float);
         pl.hist_global = pl.lds > kLdsMax || tuning(PLE_TUNE_BWD_SIMPLE_GLOBAL) == 1;
         if (pl.hist_global) pl.lds = 0;
     }
-    pl.part_bytes = static_cast<size_t>(pl.Cd) * F * B * 2 * D * sizeof(float);
-    pl.part_db_bytes = static_cast<size_t>(pl.Cd) * F * D * sizeof(float);
-    pl.part_lw_bytes = lin ? static_cast<size_t>(pl.Cd) * F * D * sizeof(float) : 0;
+    // A sorted plan of one chunk writes dW and db from the gradient kernel's
+    // LDS histogram (no chunk partials); other plans keep per-chunk partials.
+    if (!(pl.sorted && pl.C == 1)) {
+        pl.part_bytes = static_cast<size_t>(pl.Cd) * F * B * 2 * D * sizeof(float);
+        pl.part_db_bytes = static_cast<size_t>(pl.Cd) * F * D * sizeof(float);
+        pl.part_lw_bytes = lin ? static_cast<size_t>(pl.Cd) * F * D * sizeof(float) : 0;
+    }
     return pl;
 }
 
@@ -1449,15 +1452,25 @@ hipError_t launch_reduce_epi(const BwdArgs &a, int vec, dim3 grid, size_t lds, h
     constexpr int SH = EPI | kBwdShared;
     const bool shared = (static_cast<int64_t>(a.D) * esz) % 128 != 0;   // rows end inside a line
     if (vec == 8) {
-        // (16-bit gradients only, D a multiple of 8: groups of 2 to 8 lanes)
+        // (16-bit gradients only, D a multiple of 8: groups of 2 to 8 lanes;
+        // rows wider than 64 columns -- no module epilogue there -- 16 to 64)
         if constexpr (GD != PLE_DTYPE_F32) {
             switch (a.LGW) {
                 case 2: launch_bwd((ple_bwd_fused_kernel<GD, Q, 8, 2, EPI, RB>), grid, blk, lds, s, a); break;
                 case 4: launch_bwd((ple_bwd_fused_kernel<GD, Q, 8, 4, EPI, RB>), grid, blk, lds, s, a); break;
-                default:
+                case 8:
                     if (shared) launch_bwd((ple_bwd_fused_kernel<GD, Q, 8, 8, SH, RB>), grid, blk, lds, s, a);
                     else launch_bwd((ple_bwd_fused_kernel<GD, Q, 8, 8, EPI, RB>), grid, blk, lds, s, a);
                     break;
+                default:
+                    if constexpr (EPI == 0) {
+                        if (a.LGW == 16) launch_bwd((ple_bwd_fused_kernel<GD, Q, 8, 16, 0, RB>), grid, blk, lds, s, a);
+                        else if (a.LGW == 32) launch_bwd((ple_bwd_fused_kernel<GD, Q, 8, 32, 0, RB>), grid, blk, lds, s, a);
+                        else launch_bwd((ple_bwd_fused_kernel<GD, Q, 8, 64, 0, RB>), grid, blk, lds, s, a);
+                        break;
+                    } else {
+                        return hipErrorInvalidConfiguration;
+                    }
             }
             return hipGetLastError();
         } else {
@@ -1465,6 +1478,17 @@ hipError_t launch_reduce_epi(const BwdArgs &a, int vec, dim3 grid, size_t lds, h
         }
     }
     if (vec == 4) {
+        // rows of more than 64 columns (no module epilogue there): 32- and
+        // 64-lane groups
+        if (a.LGW > 16) {
+            if constexpr (EPI == 0) {
+                if (a.LGW == 32) launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 32, 0, RB>), grid, blk, lds, s, a);
+                else launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 64, 0, RB>), grid, blk, lds, s, a);
+                return hipGetLastError();
+            } else {
+                return hipErrorInvalidConfiguration;
+            }
+        }
         switch (a.LGW) {
             case 2: launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 2, EPI, RB>), grid, blk, lds, s, a); break;
             case 4: launch_bwd((ple_bwd_fused_kernel<GD, Q, 4, 4, EPI, RB>), grid, blk, lds, s, a); break;
@@ -1539,10 +1563,12 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
         a.idxb = idxb;
         // one chunk: the gradient kernel writes dW / db itself
         a.fin_fused = want_dwdb && pl.C == 1;
-        t_slot = timer_slot(PLE_TIMER_BACKWARD);
+        const TimerSlot ts = timer_slot(PLE_TIMER_BACKWARD);
+        t_slot = ts;
         e = launch_reduce<GD, Q>(a, pl.vec, epi, pl.rb, grid, pl.lds, s);
         t_slot = TimerSlot{};
         if (e != hipSuccess) return e;
+        timer_commit(ts);
     } else {
         // timed from the start of the first kernel to the end of the last
         const TimerSlot ts = timer_slot(PLE_TIMER_BACKWARD);
@@ -1561,7 +1587,8 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
         }
         if (want_dwdb) {
             t_slot = TimerSlot{want_dx ? nullptr : ts.start, ts.stop};
-            const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.F) * pl.C));
+            const int64_t col_blocks = (a.D + kWave - 1) / kWave;
+            const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.F) * pl.C * col_blocks));
             if (pl.hist_global) {
                 if (idxb == 1) launch_bwd((ple_bwd_simple_hist_kernel<GD, Q, uint8_t, true>), grid, dim3(kWave), 0, s, a);
                 else if (idxb == 2) launch_bwd((ple_bwd_simple_hist_kernel<GD, Q, int16_t, true>), grid, dim3(kWave), 0, s, a);
@@ -1574,6 +1601,7 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
             if (e != hipSuccess) return e;
         }
         t_slot = TimerSlot{};
+        timer_commit(ts);
     }
     if (want_dwdb && !(pl.sorted && a.fin_fused)) {
         size_t lds = static_cast<size_t>(a.B) * 2 * kFinStride * sizeof(float);
@@ -1648,6 +1676,22 @@ size_t backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D) {
     return need;
 }
 
+int backward_plan_info(const BackwardRequest &r, ple_backward_plan_info_t *info) {
+    const bool lin = r.lin_w != nullptr;
+    const bool raw_db = (r.quant != PLE_DTYPE_F32 && r.quant != r.grad_dtype) || lin;
+    const uintptr_t gaddr = reinterpret_cast<uintptr_t>(r.g);
+    const BwdPlan &pl = plan_cached(r.N, r.F, r.B, r.D, gaddr % 16 == 0, r.grad_dtype != PLE_DTYPE_F32, raw_db, lin);
+    info->sorted = pl.sorted ? 1 : 0;
+    info->chunks = pl.C;
+    info->features_per_group = pl.sorted ? pl.geo.FS : 1;
+    info->columns_per_lane = pl.sorted ? pl.vec : 1;
+    info->lanes_per_row = pl.sorted ? pl.geo.LGW : 1;
+    info->threads = pl.sorted ? pl.rb : kWave;
+    info->lds_bytes = pl.lds;
+    info->workspace_bytes = pl.total();
+    return PLE_OK;
+}
+
 int backward_run(const BackwardRequest &r) {
     const bool lin = r.lin_w != nullptr;
     const bool want_dx = r.dx != nullptr;
@@ -1656,6 +1700,9 @@ int backward_run(const BackwardRequest &r) {
     // module epilogues: fp32 gradient; a ReLU needs the forward's bits
     if ((r.relu || lin) && r.grad_dtype != PLE_DTYPE_F32) return PLE_E_UNSUPPORTED;
     if (r.relu && !r.mask) return PLE_E_NULL_POINTER;
+    // module epilogues: rows of at most 64 columns (the module's limit on
+    // d_embedding; the forward gathers the ReLU pass bits of a row's lanes)
+    if ((r.relu || lin) && r.D > 64) return PLE_E_TOO_LARGE;
     if (r.dlw && !lin) return PLE_E_UNSUPPORTED;
     const uintptr_t gaddr = reinterpret_cast<uintptr_t>(r.g);
     const int gbytes = r.grad_dtype == PLE_DTYPE_F32 ? 4 : 2;
@@ -1664,12 +1711,14 @@ int backward_run(const BackwardRequest &r) {
     // gradient is the sum of the buckets, as for fp32)
     const bool raw_db = (r.quant != PLE_DTYPE_F32 && r.quant != r.grad_dtype) || lin;
     const BwdPlan &pl = plan_cached(r.N, r.F, r.B, r.D, gaddr % 16 == 0, r.grad_dtype != PLE_DTYPE_F32, raw_db, lin);
-    // the sorted path always needs its descriptors; the fallback only for dW / db
-    const size_t need = (pl.sorted || want_dwdb) ? pl.total() : 0;
+    // The workspace holds chunk partials of dW / db only (the sorted path's
+    // descriptors live in LDS): dx alone needs none.
+    const size_t need = want_dwdb ? pl.total() : 0;
     if (need > 0 && (r.workspace == nullptr || r.workspace_bytes < need ||
                      reinterpret_cast<uintptr_t>(r.workspace) % 256 != 0))
         return PLE_E_WORKSPACE;
-    const int64_t grid_max = pl.sorted ? kNumXcd * tiles_per_xcd(pl.geo.G, pl.C) : static_cast<int64_t>(r.F) * pl.C;
+    const int64_t grid_max = pl.sorted ? kNumXcd * tiles_per_xcd(pl.geo.G, pl.C)
+                                       : static_cast<int64_t>(r.F) * pl.C * ((r.D + kWave - 1) / kWave);
     if (grid_max > INT32_MAX) return PLE_E_TOO_LARGE;
     BwdArgs a = pl.geo;
     a.g = r.g; a.x = r.x; a.edges = r.edges; a.iw = r.iw; a.nbins = r.nbins; a.weight = r.weight;

@@ -39,6 +39,7 @@ namespace {
 
 struct Timer {
     std::vector<hipEvent_t> ev;   // 2 * slots events: begin and end of launch i
+    std::vector<char> done;       // slot i's launch was issued (its events are recorded)
     int slots = 0;
     int used = 0;
 };
@@ -47,10 +48,15 @@ std::atomic<bool> g_timing{false};
 std::mutex g_timer_mu;
 Timer g_timers[PLE_TIMER_COUNT];
 
+// Waits for every recorded stop event (launches still in flight record
+// them), then destroys the events.
 void timers_release() {
     for (Timer &t : g_timers) {
+        for (int i = 0; i < t.used; ++i)
+            if (t.done[i]) (void)hipEventSynchronize(t.ev[2 * i + 1]);
         for (hipEvent_t e : t.ev) (void)hipEventDestroy(e);
         t.ev.clear();
+        t.done.clear();
         t.slots = t.used = 0;
     }
 }
@@ -62,9 +68,18 @@ TimerSlot timer_slot(int which) {
     std::lock_guard<std::mutex> lk(g_timer_mu);
     Timer &t = g_timers[which];
     if (t.used >= t.slots) return TimerSlot{};
-    const TimerSlot ts{t.ev[2 * t.used], t.ev[2 * t.used + 1]};
+    const TimerSlot ts{t.ev[2 * t.used], t.ev[2 * t.used + 1], which, t.used};
+    t.done[t.used] = 0;
     ++t.used;
     return ts;
+}
+
+void timer_commit(const TimerSlot &ts) {
+    if (ts.which < 0) return;
+    std::lock_guard<std::mutex> lk(g_timer_mu);
+    Timer &t = g_timers[ts.which];
+    // (a slot of timers released in the meantime is gone)
+    if (ts.index < t.used && t.ev[2 * ts.index] == ts.start) t.done[ts.index] = 1;
 }
 
 namespace {
@@ -87,7 +102,8 @@ hipError_t zero_floats(float *p, int64_t n, hipStream_t s) {
 
 int check_common(int64_t N, int64_t F, int64_t B, int64_t D) {
     if (N < 0 || F < 1 || B < 1 || D < 1) return PLE_E_BAD_SHAPE;
-    if (F > INT32_MAX / 2 || B > kMaxBins || D > 64) return PLE_E_TOO_LARGE;
+    // (the kernels index per-feature tables and rows with 32-bit offsets)
+    if (F > INT32_MAX / 2 || B > kMaxBins || D > INT32_MAX / 2) return PLE_E_TOO_LARGE;
     if (F * (B + 1) > INT32_MAX / 2 || F * B * 2 * D > INT32_MAX) return PLE_E_TOO_LARGE;
     if (N > INT64_MAX / (F * D)) return PLE_E_TOO_LARGE;
     return PLE_OK;
@@ -98,7 +114,7 @@ int check_common(int64_t N, int64_t F, int64_t B, int64_t D) {
 
 extern "C" {
 
-int ple_abi_version(void) { return (1 << 16) | 1; }
+int ple_abi_version(void) { return (1 << 16) | 2; }
 
 int ple_bin_index_bytes(int64_t max_n_bins) { return ple::idx_bytes_for(max_n_bins); }
 
@@ -117,6 +133,7 @@ int ple_timing_start(int slots) {
     if (slots == 0) return PLE_OK;
     for (ple::Timer &t : ple::g_timers) {
         t.ev.resize(2 * static_cast<size_t>(slots), nullptr);
+        t.done.assign(static_cast<size_t>(slots), 0);
         for (hipEvent_t &e : t.ev) {
             const hipError_t rc = hipEventCreate(&e);
             if (rc != hipSuccess) {
@@ -142,15 +159,18 @@ int ple_timing_read(int which, double *ms_total, int *count) {
     std::lock_guard<std::mutex> lk(ple::g_timer_mu);
     const ple::Timer &t = ple::g_timers[which];
     double sum = 0.0;
+    int n = 0;
     for (int i = 0; i < t.used; ++i) {
+        if (!t.done[i]) continue;   // (the launch was not issued)
         hipError_t rc = hipEventSynchronize(t.ev[2 * i + 1]);
         float ms = 0.0f;
         if (rc == hipSuccess) rc = hipEventElapsedTime(&ms, t.ev[2 * i], t.ev[2 * i + 1]);
         if (rc != hipSuccess) return static_cast<int>(rc);
         sum += ms;
+        ++n;
     }
     *ms_total = sum;
-    *count = t.used;
+    *count = n;
     return PLE_OK;
 }
 
@@ -161,7 +181,9 @@ const char *ple_error_string(int code) {
         case PLE_E_BAD_SHAPE: return "invalid shape (need N >= 0 and F, B, D >= 1)";
         case PLE_E_BAD_DTYPE: return "invalid dtype code";
         case PLE_E_BAD_INDEX_WIDTH: return "invalid bin index width";
-        case PLE_E_TOO_LARGE: return "sizes exceed the supported range (D <= 64, max_n_bins <= 2^24, F * max_n_bins * D < 2^30)";
+        case PLE_E_TOO_LARGE:
+            return "sizes exceed the supported range (max_n_bins <= 2^24, F * max_n_bins * D < 2^30; "
+                   "module epilogues with ReLU or linear0: D <= 64)";
         case PLE_E_WORKSPACE: return "workspace is NULL, too small or not 256-byte aligned";
         case PLE_E_UNSUPPORTED: return "combination not supported (dtype or epilogue pairing)";
         case PLE_E_MISALIGNED: return "pointer misaligned for its element type";
@@ -225,6 +247,25 @@ int ple_backward_launch(const void *grad_output, const float *x, const float *bi
     r.workspace = workspace; r.workspace_bytes = workspace_bytes;
     r.stream = s;
     return ple::backward_run(r);
+}
+
+int ple_backward_plan_query(const void *grad_output, int64_t N, int64_t F, int64_t B, int64_t D,
+                            int grad_dtype, int quant_dtype, int relu, int linear0,
+                            ple_backward_plan_info_t *info) {
+    const int rc = ple::check_common(N, F, B, D);
+    if (rc != PLE_OK) return rc;
+    if (!ple::valid_dtype(grad_dtype) || !ple::valid_dtype(quant_dtype)) return PLE_E_BAD_DTYPE;
+    if (!info) return PLE_E_NULL_POINTER;
+    if (grad_dtype != PLE_DTYPE_F32 && (quant_dtype != grad_dtype || relu || linear0)) return PLE_E_UNSUPPORTED;
+    ple::BackwardRequest r{};
+    // (any 16-byte aligned address stands for "aligned" when no gradient is given)
+    r.g = grad_output ? grad_output : reinterpret_cast<const void *>(static_cast<uintptr_t>(256));
+    static const float lin_marker = 0.0f;
+    r.lin_w = linear0 ? &lin_marker : nullptr;
+    r.relu = relu ? 1 : 0;
+    r.N = N; r.F = F; r.B = B; r.D = D;
+    r.grad_dtype = grad_dtype; r.quant = quant_dtype;
+    return ple::backward_plan_info(r, info);
 }
 
 int ple_forward_epilogue_launch(const float *x, const float *bin_edges, const float *inv_bin_widths,

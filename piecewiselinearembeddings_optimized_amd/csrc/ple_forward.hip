@@ -49,8 +49,10 @@ struct FwdArgs {
     void *idx;
     int64_t N;
     int F, B, D;
-    int FS;       // features per workgroup (power of two, FS * D/VEC <= 64)
-    int G;        // feature groups = ceil(F / FS)
+    int FS;       // features per workgroup (power of two, FS * DC/VEC <= 64)
+    int G;        // workgroup columns = ceil(F / FS) feature groups x NCC column chunks
+    int DC;       // columns per chunk (= D unless a row is wider than a wave's lanes)
+    int NCC;      // column chunks per row (FS = 1 when NCC > 1)
     int C;        // sample chunks
     int64_t NC;   // samples per chunk
     int FB;       // threads per workgroup (kBlock or 2 * kBlock)
@@ -140,14 +142,21 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
     constexpr bool LIN = EPI == kEpiLin || EPI == kEpiLinRelu;
     extern __shared__ float smem[];
     const int FS = a.FS, B = a.B, D = a.D, F = a.F;
-    const int rs = 2 * D;                                   // table row stride
-    float *tbl = smem;
-    float *sedge = tbl + static_cast<size_t>(FS) * B * rs;
-    float *siw = sedge + FS * (B + 1);
-    int *snb = reinterpret_cast<int *>(siw + FS * B);
 
     int g, c;
     if (!decode_tile(blockIdx.x, a.G, a.C, g, c)) return;
+    // A row wider than a wave's lanes is cut into column chunks, one per
+    // workgroup (one feature a group then): columns c0 .. c0 + Dw - 1 of
+    // the feature's table and output.
+    const int cc = g % a.NCC;
+    g /= a.NCC;
+    const int c0 = cc * a.DC;
+    const int Dw = min(a.DC, D - c0);
+    const int rs = 2 * Dw;                                  // table row stride
+    float *tbl = smem;
+    float *sedge = tbl + static_cast<size_t>(FS) * B * 2 * a.DC;
+    float *siw = sedge + FS * (B + 1);
+    int *snb = reinterpret_cast<int *>(siw + FS * B);
     const int f0 = g * FS;
     const int nfh = min(FS, F - f0);
     const int64_t n_begin = static_cast<int64_t>(c) * a.NC;
@@ -182,7 +191,7 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
     }
     __syncthreads();
 
-    const int U = D / VEC;
+    const int U = Dw / VEC;
     for (int i = tid; i < FS * B * U; i += FB) {
         const int fl = i / (B * U);
         const int r = i - fl * (B * U);
@@ -192,8 +201,8 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
             const int n = snb[fl];
             if (k < n) {
                 const int p = phys_bin(k, n, B);
-                const float *src = a.weight + ((static_cast<int64_t>(f0 + fl) * B + p) * D + u * VEC);
-                float *dst = tbl + (static_cast<size_t>(fl) * B + k) * rs + D + u * VEC;
+                const float *src = a.weight + ((static_cast<int64_t>(f0 + fl) * B + p) * D + c0 + u * VEC);
+                float *dst = tbl + (static_cast<size_t>(fl) * B + k) * rs + Dw + u * VEC;
                 if constexpr (VEC % 4 == 0) {
 #pragma unroll
                     for (int h = 0; h < VEC; h += 4) {
@@ -220,9 +229,9 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
     __syncthreads();
 
     // prefix over logical bins, one lane per (feature, column), in bin order
-    for (int col = tid; col < FS * D; col += FB) {
-        const int fl = col / D;
-        const int j = col - fl * D;
+    for (int col = tid; col < FS * Dw; col += FB) {
+        const int fl = col / Dw;
+        const int j = col - fl * Dw;
         if (fl < nfh) {
             const int n = snb[fl];
             float *base = tbl + static_cast<size_t>(fl) * B * rs;
@@ -231,7 +240,7 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
             for (; k + 8 <= n; k += 8) {
                 float w[8];
 #pragma unroll
-                for (int t = 0; t < 8; ++t) w[t] = base[(k + t) * rs + D + j];
+                for (int t = 0; t < 8; ++t) w[t] = base[(k + t) * rs + Dw + j];
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
                     base[(k + t) * rs + j] = acc;
@@ -239,7 +248,7 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
                 }
             }
             for (; k < n; ++k) {
-                const float w = base[k * rs + D + j];
+                const float w = base[k * rs + Dw + j];
                 base[k * rs + j] = acc;
                 acc += w;
             }
@@ -267,7 +276,7 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
     for (int t = 0; t < VEC; ++t) bvec[t] = lwv[t] = 0.0f;
     if constexpr (HAS_BIAS || LIN) {
         if (o_ok) {
-            const int64_t pofs = static_cast<int64_t>(f0 + o_fl) * D + o_u * VEC;
+            const int64_t pofs = static_cast<int64_t>(f0 + o_fl) * D + c0 + o_u * VEC;
 #pragma unroll
             for (int t = 0; t < VEC; ++t) {
                 bvec[t] = HAS_BIAS ? a.bias[pofs + t] : a.lin_b[pofs + t];
@@ -276,7 +285,8 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
         }
     }
     // ReLU bits: element j of a row is bit j % 32 of word j / 32 (a lane's
-    // VEC elements never straddle a word: VEC divides 32)
+    // VEC elements never straddle a word: VEC divides 32; the epilogues run
+    // rows of one chunk)
     const int m_shift = (o_u * VEC) & 31;
     const int m_word = (o_u * VEC) >> 5;
     const float *o_tbl = tbl + static_cast<size_t>(o_fl) * B * rs + o_u * VEC;
@@ -293,7 +303,7 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
         const int k = find_bin(v, e_row, p_n);
         const float frac = (v - e_row[k]) * iw_row[k];
         const float qf = quant<Q>(frac);
-        if (pvalid) static_cast<IdxT *>(a.idx)[pidx] = static_cast<IdxT>(k);
+        if (pvalid && cc == 0) static_cast<IdxT *>(a.idx)[pidx] = static_cast<IdxT>(k);
 
         // kStoreUnroll store instructions per step: their shuffles and table
         // reads are issued together, then the stores
@@ -317,24 +327,24 @@ __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
 #pragma unroll
                     for (int h = 0; h < VEC; h += 4) {
                         const float4 P = *reinterpret_cast<const float4 *>(row + h);
-                        const float4 W = *reinterpret_cast<const float4 *>(row + D + h);
+                        const float4 W = *reinterpret_cast<const float4 *>(row + Dw + h);
                         r[h] = fmaf(qs[q], W.x, P.x);
                         r[h + 1] = fmaf(qs[q], W.y, P.y);
                         r[h + 2] = fmaf(qs[q], W.z, P.z);
                         r[h + 3] = fmaf(qs[q], W.w, P.w);
                     }
                 } else if constexpr (VEC == 2) {
-                    // (8-byte LDS reads: D, the row stride and o_u * VEC are even)
+                    // (8-byte LDS reads: Dw, the row stride and o_u * VEC are even)
                     const float2 P = *reinterpret_cast<const float2 *>(row);
-                    const float2 W = *reinterpret_cast<const float2 *>(row + D);
+                    const float2 W = *reinterpret_cast<const float2 *>(row + Dw);
                     r[0] = fmaf(qs[q], W.x, P.x);
                     r[1] = fmaf(qs[q], W.y, P.y);
                 } else {
-                    r[0] = fmaf(qs[q], row[D], row[0]);
+                    r[0] = fmaf(qs[q], row[Dw], row[0]);
                 }
                 const bool row_ok = o_ok && s < SW && n < n_end;
                 emit_segment<Q, OUT, EPI, VEC, NT>(a, r, bvec, lwv, LIN ? xs[q] : 0.0f, row_ok,
-                                               n * row_elems + static_cast<int64_t>(f0 + o_fl) * D + o_u * VEC,
+                                               n * row_elems + static_cast<int64_t>(f0 + o_fl) * D + c0 + o_u * VEC,
                                                (n * F + f0 + o_fl) * a.MW, U, lane, o_u, m_shift, m_word);
             }
         }
@@ -382,13 +392,18 @@ __global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
     constexpr bool LIN = EPI == kEpiLin || EPI == kEpiLinRelu;
     extern __shared__ float smem[];
     const int B = a.B, D = a.D, F = a.F, S = a.S;
-    float *cp = smem;                            // [ceil(B / S)][D]
+    float *cp = smem;                            // [ceil(B / S)][DC]
     float *stage = smem + a.stage_off;           // [kWideStage]
     float *sedge = smem + a.edge_off;            // [B + 1] (edges_lds)
     float *siw = sedge + (B + 1);                // [B]     (edges_lds)
 
     int f, c;
     if (!decode_tile(blockIdx.x, a.G, a.C, f, c)) return;
+    // column chunk of rows wider than a wave's lanes (as in the table kernel)
+    const int cc = f % a.NCC;
+    f /= a.NCC;
+    const int c0 = cc * a.DC;
+    const int Dw = min(a.DC, D - c0);
     const int64_t n_begin = static_cast<int64_t>(c) * a.NC;
     const int64_t n_end = min(a.N, n_begin + a.NC);
     if (n_begin >= n_end) return;
@@ -407,23 +422,25 @@ __global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
     // Weight rows 0..n-2 enter prefixes (the prefix of bin k sums bins < k,
     // all identity-mapped below the last bin).  Blocks of kb bins are staged
     // (contiguous rows of W), then the threads of columns 0..D-1 fold them.
-    const int kb = kWideStage / D;
+    const int kb = kWideStage / Dw;
     float acc = 0.0f;
     int next_cp = 0, m_cp = 0;
     for (int k0 = 0; k0 < n; k0 += kb) {
         const int nk = min(kb, n - k0);
         const int nterm = min(nk, n - 1 - k0);       // rows of this block that enter a prefix
-        for (int i = tid; i < nk * D; i += kWideFB)
-            stage[i] = i < nterm * D ? quant<Q>(wf[static_cast<int64_t>(k0) * D + i]) : 0.0f;
+        for (int i = tid; i < nk * Dw; i += kWideFB) {
+            const int t = i / Dw;
+            stage[i] = t < nterm ? quant<Q>(wf[static_cast<int64_t>(k0 + t) * D + c0 + (i - t * Dw)]) : 0.0f;
+        }
         __syncthreads();
-        if (tid < D) {
+        if (tid < Dw) {
             for (int t = 0; t < nk; ++t) {
                 if (k0 + t == next_cp) {
-                    cp[m_cp * D + tid] = acc;
+                    cp[m_cp * Dw + tid] = acc;
                     ++m_cp;
                     next_cp += S;
                 }
-                acc += stage[t * D + tid];
+                acc += stage[t * Dw + tid];
             }
         }
         __syncthreads();
@@ -432,7 +449,7 @@ __global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
     // ---- stream wave tiles (one sample a lane, then rows of U lanes) -------
     const int wave = tid / kWave;
     const int lane = tid % kWave;
-    const int U = D / VEC;
+    const int U = Dw / VEC;
     const int R = kWave / U;
     const float *e_row = a.edges_lds ? sedge : ef;
     const float *iw_row = a.edges_lds ? siw : iwf;
@@ -444,7 +461,7 @@ __global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
     for (int t = 0; t < VEC; ++t) bvec[t] = lwv[t] = 0.0f;
     if constexpr (HAS_BIAS || LIN) {
         if (o_ok) {
-            const int64_t pofs = static_cast<int64_t>(f) * D + o_u * VEC;
+            const int64_t pofs = static_cast<int64_t>(f) * D + c0 + o_u * VEC;
 #pragma unroll
             for (int t = 0; t < VEC; ++t) {
                 bvec[t] = HAS_BIAS ? a.bias[pofs + t] : a.lin_b[pofs + t];
@@ -454,7 +471,7 @@ __global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
     }
     const int m_shift = (o_u * VEC) & 31;
     const int m_word = (o_u * VEC) >> 5;
-    const float *wcol = wf + o_u * VEC;            // this lane's columns of W[f]
+    const float *wcol = wf + c0 + o_u * VEC;       // this lane's columns of W[f]
     const int64_t rows = n_end - n_begin;
     const int64_t n_tiles = (rows + kWave - 1) / kWave;
     const int64_t row_elems = static_cast<int64_t>(F) * D;
@@ -466,7 +483,7 @@ __global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
         const float v = pvalid ? a.x[pn * F + f] : 0.0f;
         const int k = find_bin(v, e_row, n);
         const float qf = quant<Q>((v - e_row[k]) * iw_row[k]);
-        if (pvalid) static_cast<IdxT *>(a.idx)[pn * F + f] = static_cast<IdxT>(k);
+        if (pvalid && cc == 0) static_cast<IdxT *>(a.idx)[pn * F + f] = static_cast<IdxT>(k);
 
         for (int sb = 0; sb < kWave; sb += R) {
             const int s = sb + o_s;
@@ -480,7 +497,7 @@ __global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
             if (row_ok) {
                 const int m = ks / S;
                 float P[VEC], W[VEC];
-                lds_load_vec<VEC>(cp + m * D + o_u * VEC, P);
+                lds_load_vec<VEC>(cp + m * Dw + o_u * VEC, P);
                 for (int i = m * S; i < ks; ++i) {
                     const float *wi = wcol + static_cast<int64_t>(i) * D;
 #pragma unroll
@@ -495,7 +512,7 @@ __global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
 #pragma unroll
                 for (int h = 0; h < VEC; ++h) r[h] = 0.0f;
             }
-            emit_segment<Q, OUT, EPI, VEC>(a, r, bvec, lwv, xs, row_ok, nn * row_elems + static_cast<int64_t>(f) * D + o_u * VEC,
+            emit_segment<Q, OUT, EPI, VEC>(a, r, bvec, lwv, xs, row_ok, nn * row_elems + static_cast<int64_t>(f) * D + c0 + o_u * VEC,
                                            (nn * F + f) * a.MW, U, lane, o_u, m_shift, m_word);
         }
     }
@@ -512,6 +529,7 @@ constexpr int kOutPerTable = 10;
 
 struct FwdPlan {
     int vec, FS, G, C, FB;
+    int DC = 0, NCC = 1;                // column chunks (rows wider than a wave's lanes)
     int64_t NC;
     size_t lds;
     bool wide = false;                  // ple_fwd_wide_kernel
@@ -524,24 +542,34 @@ struct FwdPlan {
 constexpr size_t kWideCpBudget = 96 * 1024;
 constexpr size_t kWideEdgeBudget = 40 * 1024;
 
+// Rows of more than a wave's lanes (D / vec > 64) are cut into NCC chunks of
+// DC columns (a multiple of vec), as even as the lanes allow.
+void plan_chunks(int64_t D, FwdPlan &pl) {
+    const int64_t U = D / pl.vec;
+    pl.NCC = static_cast<int>((U + kWave - 1) / kWave);
+    pl.DC = static_cast<int>((U + pl.NCC - 1) / pl.NCC) * pl.vec;
+}
+
 void plan_wide(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, FwdPlan &pl) {
     pl.wide = true;
     pl.FS = 1;
     pl.FB = kWideFB;
     if (pl.vec == 8) pl.vec = 4;
-    int64_t S = (B * D * 4 + static_cast<int64_t>(kWideCpBudget) - 1) / static_cast<int64_t>(kWideCpBudget);
+    plan_chunks(D, pl);
+    const int64_t Dc = pl.DC;
+    int64_t S = (B * Dc * 4 + static_cast<int64_t>(kWideCpBudget) - 1) / static_cast<int64_t>(kWideCpBudget);
     if (S < 1) S = 1;
     const int64_t ncp = (B + S - 1) / S;
     pl.S = static_cast<int>(S);
-    pl.stage_off = static_cast<int>(align_up(static_cast<size_t>(ncp * D), 4));
+    pl.stage_off = static_cast<int>(align_up(static_cast<size_t>(ncp * Dc), 4));
     pl.edge_off = pl.stage_off + kWideStage;
     pl.edges_lds = static_cast<size_t>(2 * B + 1) * 4 <= kWideEdgeBudget ? 1 : 0;
     pl.lds = 4 * (static_cast<size_t>(pl.edge_off) + (pl.edges_lds ? static_cast<size_t>(2 * B + 1) : 0));
-    pl.G = static_cast<int>(F);
+    pl.G = static_cast<int>(F) * pl.NCC;
     // chunks: about two workgroups per CU over the grid, each writing at least
     // kOutPerTable times the weight bytes its prefix pass reads
     const int64_t target = 2 * static_cast<int64_t>(device_cu_count());
-    int64_t c = (target + F - 1) / F;
+    int64_t c = (target + pl.G - 1) / pl.G;
     const int64_t min_nc = (static_cast<int64_t>(kOutPerTable) * B * 4 + out_bytes - 1) / out_bytes;
     const int64_t c_tbl = (N + min_nc - 1) / min_nc;
     if (c > c_tbl) c = c_tbl;
@@ -571,14 +599,17 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
     // instructions and table reads of one per lane
     pl.vec = (D % 4 == 0 && aligned16) ? 4 : ((D % 2 == 0 && aligned16 && tuning(PLE_TUNE_FWD_VEC) != 1) ? 2 : 1);
     if (out_bytes == 2 && D % 8 == 0 && aligned16 && out16 && tuning(PLE_TUNE_FWD_VEC) != 4) pl.vec = 8;
-    const int U = static_cast<int>(D / pl.vec);
-    if (U > kWave) return false;
-    if (fwd_lds_bytes(1, B, D) > kLdsMax || tuning(PLE_TUNE_FWD_WIDE) == 1) {
+    plan_chunks(D, pl);
+    if (fwd_lds_bytes(1, B, pl.DC) > kLdsMax || tuning(PLE_TUNE_FWD_WIDE) == 1) {
         plan_wide(N, F, B, D, out_bytes, pl);
         return true;
     }
-    const int Bi = static_cast<int>(B), Di = static_cast<int>(D);
-    auto fits_wave = [&](int f) { return f <= kWave && f * U <= kWave && (f == 1 || f / 2 < F); };
+    // (rows of several chunks: one feature a group; D below is a chunk's width)
+    const int U = pl.DC / pl.vec;
+    const int Bi = static_cast<int>(B), Di = pl.DC;
+    auto fits_wave = [&](int f) {
+        return f <= kWave && f * U <= kWave && (f == 1 || f / 2 < F) && (f == 1 || pl.NCC == 1);
+    };
     int fs = 1;
     while (fits_wave(fs * 2) && fwd_lds_bytes(fs * 2, Bi, Di) <= kLdsBudget) fs *= 2;
     // Rows of up to 24 columns run 512-thread workgroups (below), whose waves
@@ -595,11 +626,11 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
     // 298 us, d = 50 650 -> 450 us, d = 56 793 -> 372 us, d = 62 741 -> 544
     // us, d = 64 390 -> 340 us)
     if (fs == 1 && fits_wave(2) && fwd_lds_bytes(2, Bi, Di) <= 2 * kLdsBudget) fs = 2;
-    while (static_cast<int64_t>(fs) * D * out_bytes < 128 && fits_wave(fs * 2) &&
+    while (static_cast<int64_t>(fs) * Di * out_bytes < 128 && fits_wave(fs * 2) &&
            fwd_lds_bytes(fs * 2, Bi, Di) <= kLdsMax)
         fs *= 2;
     const int fs_env = tuning(PLE_TUNE_FWD_FS);
-    if (fs_env > 0 && (fs_env & (fs_env - 1)) == 0 && fs_env * U <= kWave &&
+    if (fs_env > 0 && (fs_env & (fs_env - 1)) == 0 && fits_wave(fs_env) &&
         fwd_lds_bytes(fs_env, Bi, Di) <= kLdsMax)
         fs = fs_env;
     pl.lds = fwd_lds_bytes(fs, Bi, Di);
@@ -611,11 +642,11 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
     // (F=128, 48 bins, N=65536 unless named): c4 204 -> 151 us, c3 157 -> 125
     // us, d=12 97 -> 86 us, d=24 184 -> 175 us; d=32 (c1) and d=48 the same,
     // d=64 +7 us.  PLE_TUNE_FWD_FB overrides it.
-    pl.FB = (kLdsMax / pl.lds < 3 || D <= 24) ? 2 * kBlock : kBlock;
+    pl.FB = (kLdsMax / pl.lds < 3 || Di <= 24) ? 2 * kBlock : kBlock;
     const int fb_env = tuning(PLE_TUNE_FWD_FB);
     if (fb_env == kBlock || fb_env == 2 * kBlock) pl.FB = fb_env;
     pl.FS = fs;
-    pl.G = static_cast<int>((F + fs - 1) / fs);
+    pl.G = static_cast<int>((F + fs - 1) / fs) * pl.NCC;
     const int wg_env = tuning(PLE_TUNE_FWD_WG_PER_CU);
     const int64_t target = static_cast<int64_t>(wg_env > 0 ? wg_env : 32) * device_cu_count();
     int64_t c = (target + pl.G - 1) / pl.G;
@@ -727,6 +758,10 @@ int forward_run(const ForwardRequest &r) {
     if (r.bias && r.lin_w) return PLE_E_UNSUPPORTED;
     if (r.lin_w && !r.lin_b) return PLE_E_NULL_POINTER;
     if (r.relu && !r.bias && !r.lin_w) return PLE_E_UNSUPPORTED;
+    // module epilogues with ReLU or linear0: rows of at most 64 columns (the
+    // module's limit on d_embedding; the ReLU pass bits are gathered from one
+    // row's lanes)
+    if ((r.relu || r.lin_w) && r.D > 64) return PLE_E_TOO_LARGE;
     const int epi = r.bias ? (r.relu ? kEpiBiasRelu : kEpiBias)
                   : r.lin_w ? (r.relu ? kEpiLinRelu : kEpiLin) : kEpiNone;
     if (epi != kEpiNone ? r.out_dtype != PLE_DTYPE_F32 : r.out_dtype != r.quant) return PLE_E_UNSUPPORTED;
@@ -744,6 +779,7 @@ int forward_run(const ForwardRequest &r) {
     a.out = r.out; a.idx = r.idx;
     a.N = r.N; a.F = static_cast<int>(r.F); a.B = static_cast<int>(r.B); a.D = static_cast<int>(r.D);
     a.FS = pl.FS; a.G = pl.G; a.C = pl.C; a.NC = pl.NC; a.FB = pl.FB;
+    a.DC = pl.DC; a.NCC = pl.NCC;
     // A feature group's outputs of a sample are one segment of FS * D
     // outputs; the neighbouring group writes the rest of its first and last
     // lines.  Streaming stores suit segments whose ends fall on 64-byte
@@ -752,7 +788,7 @@ int forward_run(const ForwardRequest &r) {
     // the lines first (F = 128, 48 bins, N = 65536: d = 28 fp32 380 -> 298 us,
     // d = 44 504 -> 409 us; at 64-byte ends plain stores lost 15-35%).
     {
-        const int64_t seg = static_cast<int64_t>(pl.FS) * r.D * out_bytes;
+        const int64_t seg = static_cast<int64_t>(pl.FS) * pl.DC * out_bytes;
         const int64_t row = r.F * r.D * out_bytes;
         a.out_nt = seg % 64 == 0 && row % 64 == 0 && reinterpret_cast<uintptr_t>(r.out) % 64 == 0;
     }
@@ -767,6 +803,8 @@ int forward_run(const ForwardRequest &r) {
         case PLE_DTYPE_F16: e = launch_q<PLE_DTYPE_F16>(a, epi, pl.vec, idxb, pl.wide, dim3(grid), pl.lds, r.stream); break;
         default: e = launch_q<PLE_DTYPE_BF16>(a, epi, pl.vec, idxb, pl.wide, dim3(grid), pl.lds, r.stream); break;
     }
+    if (e == hipSuccess) timer_commit(t_slot);
+    t_slot = TimerSlot{};
     return e == hipSuccess ? PLE_OK : static_cast<int>(e);
 }
 

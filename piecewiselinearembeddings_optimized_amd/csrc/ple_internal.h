@@ -26,13 +26,18 @@ uint32_t tuning_epoch();
 
 // Kernel timing (ple_timing_*): the start / stop events of the next timed
 // launch of timer `which` (PLE_TIMER_*), or two NULLs when timing is off or
-// its slots are used up; the slot counts as used.  The events go to
-// hipExtLaunchKernelGGL, which records them at the kernel's start and end.
+// its slots are used up.  The events go to hipExtLaunchKernelGGL, which
+// records them at the kernel's start and end; the launcher then commits the
+// slot (timer_commit), and only committed slots are read back, so a launch
+// that was never issued leaves no unrecorded events behind.
 struct TimerSlot {
     hipEvent_t start = nullptr;
     hipEvent_t stop = nullptr;
+    int which = -1;
+    int index = -1;
 };
 TimerSlot timer_slot(int which);
+void timer_commit(const TimerSlot &ts);
 
 inline int idx_bytes_for(int64_t B) { return B <= 256 ? 1 : (B <= 32768 ? 2 : 4); }
 
@@ -76,6 +81,9 @@ struct BackwardRequest {
 
 size_t backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D);
 int backward_run(const BackwardRequest &r);
+// The plan backward_run would take (r's pointers other than g and the
+// outputs are not read).
+int backward_plan_info(const BackwardRequest &r, ple_backward_plan_info_t *info);
 
 struct EncodeRequest {
     const float *x, *edges, *iw;

@@ -71,7 +71,8 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     dummy = p(256)
     args = [dummy] * 5 + [None, dummy, dummy]
     assert lib.ple_forward_launch(*args, 4, 0, 3, 2, 0, 0, None) == -2       # F = 0
-    assert lib.ple_forward_launch(*args, 4, 2, 3, 65, 0, 0, None) == -5      # D > 64
+    assert lib.ple_forward_launch(*args, 0, 2, 3, 65, 0, 0, None) == 0       # D > 64: accepted (any D)
+    assert lib.ple_forward_launch(*args, 4, 2, 3, 1 << 29, 0, 0, None) == -5  # F * B * 2D beyond int32 offsets
     assert lib.ple_forward_launch(*args, 4, 2, (1 << 24) + 1, 2, 0, 0, None) == -5   # max bins > 2^24
     assert lib.ple_forward_launch(*args, 0, 2, 40000, 4, 0, 0, None) == 0    # int32 indices: accepted
     assert lib.ple_forward_launch(*args, 0, 2, 32768, 64, 0, 0, None) == 0   # tables far beyond LDS: accepted
@@ -97,9 +98,34 @@ def test_ctypes_binding_declares_the_header_and_maps_errors():
     assert ei.value.code == -7
     assert capi.workspace_bytes(0, 2, 3, 4) == 0
     assert capi.workspace_bytes(1024, 8, 48, 24) > 0
-    assert capi.workspace_bytes(1024, 8, 48, 65) == 0      # rejected sizes need nothing
+    assert capi.workspace_bytes(1024, 8, 48, 1 << 29) == 0   # rejected sizes need nothing
+    assert capi.workspace_bytes(4096, 8, 48, 96) > 0         # wider rows than the module's: accepted
     # tables beyond LDS: the fallback's chunk partials
     assert capi.workspace_bytes(2048, 4, 40000, 4) >= 4 * 40000 * 2 * 4 * 4
+
+
+def test_backward_plan_query_and_workspace_sizes():
+    """The plan query needs no device (the planner assumes 256 CUs without
+    one, as on an MI355X), and the workspace holds chunk partials only: a
+    sorted plan of one chunk -- more feature groups than resident
+    workgroups -- writes dW / db from the gradient kernel and needs none."""
+    from piecewiselinearembeddings_optimized_amd import capi
+
+    one = capi.backward_plan(1024, 8192, 48, 32)
+    assert one["sorted"] == 1 and one["chunks"] == 1
+    assert one["workspace_bytes"] == 0
+    assert capi.workspace_bytes(1024, 8192, 48, 32) == 0
+    c1 = capi.backward_plan(65536, 128, 48, 32)      # the headline shape: several chunks
+    assert c1["sorted"] == 1 and c1["chunks"] > 1
+    assert c1["features_per_group"] * c1["lanes_per_row"] >= 1 and c1["columns_per_lane"] == 4
+    assert c1["workspace_bytes"] >= c1["chunks"] * 128 * 48 * 2 * 32 * 4
+    assert capi.workspace_bytes(65536, 128, 48, 32) >= c1["workspace_bytes"]
+    c4 = capi.backward_plan(8192, 1024, 96, 24, grad_dtype=torch.bfloat16)
+    assert c4["sorted"] == 1 and c4["chunks"] == 1 and c4["columns_per_lane"] == 8
+    wide = capi.backward_plan(2048, 4, 40000, 4)    # tables beyond LDS: the fallback kernels
+    assert wide["sorted"] == 0 and wide["workspace_bytes"] >= 4 * 40000 * 2 * 4 * 4
+    with pytest.raises(capi.PleError):
+        capi.backward_plan(1024, 8, 48, 24, grad_dtype=torch.bfloat16, quant_dtype=torch.float16)
 
 
 def test_timing_api_without_a_device():

@@ -130,8 +130,19 @@ def test_c_abi_rejects_before_launch_on_device(capi):
     g = torch.randn((n, f, d), device=DEV)
     gw = torch.empty((f, bmax, d), device=DEV)
     small = torch.empty(16, dtype=torch.uint8, device=DEV)
+    # (one chunk here: dW from the gradient kernel, no workspace needed)
+    assert capi.workspace_bytes(n, f, bmax, d) == 0
+    capi.backward(g, x, e, iw, nb, wt, idx, None, gw, None, torch.float32, workspace=small)
+    # several chunks: partials in the workspace
+    w2 = workloads.make(0, 4096)
+    n2 = w2.shape[0]
+    x2 = _t(w2.x)
+    idx2 = torch.empty((n2, f), dtype=torch.uint8, device=DEV)
+    capi.forward(x2, e, iw, nb, wt, None, torch.empty((n2, f, d), device=DEV), idx2, torch.float32)
+    assert capi.workspace_bytes(n2, f, bmax, d) > 16
     with pytest.raises(capi.PleError) as ei:      # workspace too small
-        capi.backward(g, x, e, iw, nb, wt, idx, None, gw, None, torch.float32, workspace=small)
+        capi.backward(torch.randn((n2, f, d), device=DEV), x2, e, iw, nb, wt, idx2, None, gw, None, torch.float32,
+                      workspace=small)
     assert ei.value.code == -6
     with pytest.raises(capi.PleError) as ei:      # bf16 gradient with fp32 quantisation
         capi.backward(g.to(torch.bfloat16), x, e, iw, nb, wt, idx, None, gw, None, torch.float32)

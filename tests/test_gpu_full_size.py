@@ -182,3 +182,91 @@ def test_full_size_backward(cfg):
         rel = normwise_rel(s_.cpu().numpy(), (a_.double() + b_.double()).cpu().numpy())
         print(f"  linearity {name}: normwise relative error {rel:.3g}", flush=True)
         assert rel <= 1e-5
+
+
+@pytest.fixture(scope="module")
+def c4():
+    assert torch.cuda.is_available(), "HIP device required"
+    import piecewiselinearembeddings_optimized_amd  # noqa: F401  (registers the ops)
+
+    w = workloads.make(4)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)  # noqa: E731
+    ins = (t(w.x), t(w.edges), t(w.inv_widths), t(w.n_bins), t(w.weight), t(w.bias))
+    yield w, ins, torch.ops.rtdl_num_embeddings_cuda
+    del ins
+    torch.cuda.empty_cache()
+
+
+def test_full_size_c4_with_bias(c4, c_oracle):
+    """c4 as its configuration names it, with the bias b: the fused-bias
+    operators with bf16 quantisation (the reference module under bf16 autocast,
+    reference module.py:238-239: x_ple in bf16, + b in fp32).  Forward: sampled
+    rows bit-exact against the C mirror (bf16-rounded x_ple, then + b in fp32).
+    Backward with an fp32 gradient: dx and dW use the gradient rounded to bf16
+    (at the bf16 bar of the bf16-aware closed form), db is the sum of the
+    unrounded gradient (at the fp32 bar)."""
+    w, (x, e, iw, nb, wt, bt), ops = c4
+    n, f, bmax, d = w.shape
+    print(f"full-size c4 with bias shape={w.shape}", flush=True)
+    out, idx = ops.forward_with_bias(x, e, iw, nb, wt, bt, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32
+    np.testing.assert_array_equal(idx.cpu().numpy().astype(np.int64), po.bin_indices(w.x, w.edges, w.n_bins))
+    rows = np.sort(np.random.default_rng(12).choice(n, 256, replace=False))
+    mirror, _ = c_oracle.forward_f32(w.x[rows], w.edges, w.inv_widths, w.n_bins, w.weight, bias=w.bias, quant="bf16")
+    got = out[torch.from_numpy(rows).to(DEV)].cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), mirror.view(np.uint32))
+    del out
+
+    g = torch.randn((n, f, d), device=DEV, generator=torch.Generator(DEV).manual_seed(7))
+    gx, gw, gb = ops.backward_with_bias(g, x, e, iw, nb, wt, idx, torch.bfloat16, True, True, True)
+    gx2, gw2, gb2 = ops.backward_with_bias(g, x, e, iw, nb, wt, idx, torch.bfloat16, True, True, True)
+    torch.cuda.synchronize()
+    assert torch.equal(gx, gx2) and torch.equal(gw, gw2) and torch.equal(gb, gb2)
+    del gx2, gw2, gb2
+    gq = g.bfloat16().float()
+    dx, dx_abs, dw, dw_abs, _, _ = _reference_backward(x, e, iw, nb, wt, idx, gq, torch.bfloat16)
+    for name, got_, ref, s in (("dx", gx, dx, dx_abs), ("dW", gw, dw, dw_abs)):
+        _report(name, *close_scaled(got_.cpu().numpy(), ref.cpu().numpy(), s.cpu().numpy(), BF16_RTOL, 0.0))
+    del dx, dx_abs, dw, dw_abs
+    db = g.double().sum(0)
+    db_abs = g.double().abs().sum(0)
+    _report("db (unrounded gradient)", *close_scaled(gb.cpu().numpy(), db.cpu().numpy(), db_abs.cpu().numpy(),
+                                                     FP32_RTOL, FP32_ATOL))
+
+
+def test_full_size_c4_module_under_bf16_autocast(c4):
+    """The module (version A, with its bias) at c4 size under bf16 autocast,
+    as the reference module runs it there (module.py:145-158, 238-239): the
+    output is fp32, its gradients land in .grad -- x.grad and weight.grad at
+    the bf16 bar of the bf16-aware float64 closed form (the gradient reaches
+    the operator rounded to bf16), bias.grad at the fp32 bar of the sum of the
+    unrounded gradient."""
+    from rtdl_num_embeddings_cuda import CudaPiecewiseLinearEmbeddings
+
+    w, (x, e, iw, nb, wt, bt), ops = c4
+    n, f, bmax, d = w.shape
+    print(f"full-size c4 module under bf16 autocast shape={w.shape}", flush=True)
+    bins = [torch.from_numpy(w.edges[j, : int(w.n_bins[j]) + 1].copy()) for j in range(f)]
+    m = CudaPiecewiseLinearEmbeddings(bins, d, activation=False, version="A").to(DEV)
+    with torch.no_grad():
+        m.linear.weight.copy_(wt)
+        m.linear.bias.copy_(bt)
+    xr = x.clone().requires_grad_(True)
+    g = torch.randn((n, f, d), device=DEV, generator=torch.Generator(DEV).manual_seed(8))
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = m(xr)
+    assert out.dtype == torch.float32
+    out.backward(g)
+    torch.cuda.synchronize()
+    # (the module's own padded tables: its inverse widths are its own computation)
+    me, miw, mnb = m._cuda_bin_edges, m._cuda_inv_bin_widths, m._cuda_n_bins
+    _, idx = ops.forward(x, me, miw, mnb, wt, torch.bfloat16)
+    gq = g.bfloat16().float()
+    dx, dx_abs, dw, dw_abs, _, _ = _reference_backward(x, me, miw, mnb, wt, idx, gq, torch.bfloat16)
+    for name, got_, ref, s in (("x.grad", xr.grad, dx, dx_abs), ("weight.grad", m.linear.weight.grad, dw, dw_abs)):
+        _report(name, *close_scaled(got_.cpu().numpy(), ref.cpu().numpy(), s.cpu().numpy(), BF16_RTOL, 0.0))
+    del dx, dx_abs, dw, dw_abs
+    db = g.double().sum(0)
+    _report("bias.grad", *close_scaled(m.linear.bias.grad.cpu().numpy(), db.cpu().numpy(),
+                                       g.double().abs().sum(0).cpu().numpy(), FP32_RTOL, FP32_ATOL))
