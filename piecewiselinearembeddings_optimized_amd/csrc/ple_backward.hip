@@ -89,7 +89,7 @@ struct BwdArgs {
     // sorted path
     int FS, G, NT, T, SPC, PM, LGW;   // T sub-tiles, SPC sub-tiles per chunk, PM piece capacity
     int ro_qw, ro_hist, ro_db, ro_iw, ro_nb, ro_desc, ro_piece, ro_npc, ro_rec, ro_rkey, ro_rfl, ro_dx,
-        ro_lw, ro_dlw, ro_edge, ro_cnt, ro_seg, ro_tmp;   // fused kernel LDS (ro_dx < 0: no dx staging)
+        ro_lw, ro_dlw, ro_xs, ro_edge, ro_cnt, ro_seg, ro_tmp;   // fused kernel LDS (ro_dx < 0: no dx staging)
 };
 
 constexpr int kP = 1024;                        // (sample, feature) pairs per sub-tile
@@ -271,10 +271,13 @@ __device__ __forceinline__ void tile_rank(const BwdArgs &a, int t, int nfh, int 
     }
 }
 
-template <int RB>
+// kX: also x of every pair (xk, as ranked) to xs[sorted slot] (the linear0
+// epilogue's per-row x).
+template <int RB, bool kX = false>
 __device__ __forceinline__ void tile_place(const BwdArgs &a, int tid, const int (&ko)[kP / RB],
                                            const uint32_t (&qb)[kP / RB], uint16_t *s_cnt, int *s_seg, int *s_tmp,
-                                           uint2 *desc, uint32_t *piece, int *npc) {
+                                           uint2 *desc, uint32_t *piece, int *npc, const float (&xk)[kP / RB],
+                                           float *xs) {
     constexpr int kPR = kP / RB;
     const int FS = a.FS, B = a.B;
     const int fs_shift = __ffs(FS) - 1;
@@ -342,6 +345,7 @@ __device__ __forceinline__ void tile_place(const BwdArgs &a, int tid, const int 
             const int within = s_cnt[(p >> 6) * CS + key] + (ko[u] >> 16);
             const int slot = (st & 0xffff) + within;
             desc[slot] = make_uint2(qb[u], static_cast<uint32_t>(s) | (static_cast<uint32_t>(fl) << 24));
+            if constexpr (kX) xs[slot] = xk[u];
             if (within % kL == 0) {
                 const int cnt = (s_seg[key + 1] & 0xffff) - (st & 0xffff);
                 const int rows = min(kL, cnt - within);
@@ -365,12 +369,15 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     constexpr bool kLin = (EPI & kBwdLin) != 0;
     // A gradient that arrives in the quantisation dtype (or fp32 rounding)
     // is its own rounding: rounding it again changes nothing, and the bias
-    // gradient is then the sum of the bin buckets (taken at finalize).
-    // Otherwise -- an fp32 gradient rounded to 16 bits, or the linear0
-    // branch -- the bias gradient needs its own sum of the unrounded (for
-    // linear0: unmasked) gradient.
+    // gradient is then the sum of the bin buckets (taken at finalize) -- also
+    // linear0's bias gradient without a ReLU, whose buckets sum the unmasked
+    // gradient.  Otherwise -- an fp32 gradient rounded to 16 bits, or linear0
+    // behind a ReLU -- the bias gradient needs its own sum of the unrounded
+    // (unmasked) gradient.  kFeatSums: per-feature sums in the records (that
+    // one, and linear0's sum of g x).
     constexpr bool kGradExact = GD == Q || Q == PLE_DTYPE_F32;
-    constexpr bool kRawDb = !kGradExact || kLin;
+    constexpr bool kRawDb = !kGradExact || (kLin && kRelu);
+    constexpr bool kFeatSums = kRawDb || kLin;
     extern __shared__ __align__(16) unsigned char lds[];
     const int FS = a.FS, B = a.B, D = a.D, F = a.F, NT = a.NT;
     float *s_qw = reinterpret_cast<float *>(lds + a.ro_qw);             // [FS][B][D] q(W) * iw
@@ -390,9 +397,10 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     int *s_tmp = reinterpret_cast<int *>(lds + a.ro_tmp);               // [RB/64] (sort)
     float *s_rec = reinterpret_cast<float *>(lds + a.ro_rec);           // [LG][RS]
     int *s_rkey = reinterpret_cast<int *>(lds + a.ro_rkey);             // [LG]
-    int *s_rfl = reinterpret_cast<int *>(lds + a.ro_rfl);               // [LG] (kRawDb)
+    int *s_rfl = reinterpret_cast<int *>(lds + a.ro_rfl);               // [LG] (kFeatSums)
     float *s_lw = reinterpret_cast<float *>(lds + a.ro_lw);             // [FS][D] linear0 weight
     float *s_dlw = reinterpret_cast<float *>(lds + a.ro_dlw);           // [FS][D] sum of g x
+    float *s_xs = reinterpret_cast<float *>(lds + a.ro_xs);             // [P+1] x of the sorted rows (linear0)
 
     int g, c;
     if (!decode_tile(blockIdx.x, a.G, a.C, g, c)) return;
@@ -415,11 +423,15 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     load_pairs(t_begin);
     int ko[kP / RB];          // the next sub-tile's keys | ranks, and q(frac) bits
     uint32_t qb[kP / RB];
+    float xk[kP / RB];        // (linear0: their x)
 
     // ---- stage tables, clear accumulators ---------------------------------
     // Rows past a piece's end read the dummy row kP: q(frac) = +0 and sample
     // NT, whose gradient offset lies past every sub-tile's span (zeros).
     if (tid == 0) s_sdesc[kP] = make_uint2(0u, static_cast<uint32_t>(NT));
+    if constexpr (kLin) {
+        if (tid == 0) s_xs[kP] = 0.0f;   // (rows past a piece's end)
+    }
     for (int i = tid; i < FS; i += NTH) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
     for (int i = tid; i < FS * B; i += NTH) {
         const int fl = i / B;
@@ -457,8 +469,10 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     // the first sub-tile's sort (the tables it reads are staged before the
     // barrier above), then the next sub-tile's pairs
     tile_rank<Q, RB>(a, t_begin, nfh, tid, pk, pv, s_nb, s_edge, s_iw, s_cnt, ko, qb);
+#pragma unroll
+    for (int u = 0; u < kP / RB; ++u) xk[u] = kLin ? pv[u] : 0.0f;
     __syncthreads();
-    tile_place<RB>(a, tid, ko, qb, s_cnt, s_seg, s_tmp, s_sdesc, s_piece, s_npc);
+    tile_place<RB, kLin>(a, tid, ko, qb, s_cnt, s_seg, s_tmp, s_sdesc, s_piece, s_npc, xk, s_xs);
     if (t_begin + 1 < t_end) load_pairs(t_begin + 1);
     __syncthreads();
 
@@ -471,6 +485,7 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     const int D2 = 2 * D;
     // record stride {bucket | weighted (| raw g) (| g x)}
     const int RS = (kRawDb ? 3 * D : 2 * D) + (kLin ? D : 0);
+    const int off_ax = D2 + (kRawDb ? D : 0);   // record offset of the g x sums (linear0)
     // dx of sorted row j: dword 2 j of the descriptors (row kP + 1 takes the
     // rows past a piece's end)
     uint32_t *s_dxw = reinterpret_cast<uint32_t *>(s_sdesc);
@@ -494,6 +509,38 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     // nothing and need no masking.
     int key0 = -1, fl0 = -1;
     float *rec = s_rec + lg * RS + lc * VEC;
+    // Per-feature sums of the epilogue kernels (raw bias gradient, linear0's
+    // g x) run in registers across the run's pieces and go to LDS when the
+    // feature changes (rarely: a run spans at most FS features) and at the
+    // run's end -- the first feature into the record, others into s_db /
+    // s_dlw (this run is their only writer).
+    int cur_fl = -1;
+    float ad_run[VEC], ax_run[VEC];
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) ad_run[q] = ax_run[q] = 0.0f;
+    auto flush_feat = [&]() __attribute__((always_inline)) {
+        if constexpr (kFeatSums) {
+            if (cur_fl >= 0 && c_ok) {
+                const bool first = cur_fl == fl0;
+                if constexpr (kRawDb) {
+                    float *dstd = first ? rec + D2 : s_db + __umul24(cur_fl, D) + lc * VEC;
+                    float hd[VEC];
+                    lds_load_vec<VEC>(dstd, hd);
+#pragma unroll
+                    for (int q = 0; q < VEC; ++q) hd[q] += ad_run[q];
+                    lds_store_vec<VEC>(dstd, hd);
+                }
+                if constexpr (kLin) {
+                    float *dstx = first ? rec + off_ax : s_dlw + __umul24(cur_fl, D) + lc * VEC;
+                    float hx[VEC];
+                    lds_load_vec<VEC>(dstx, hx);
+#pragma unroll
+                    for (int q = 0; q < VEC; ++q) hx[q] += ax_run[q];
+                    lds_store_vec<VEC>(dstx, hx);
+                }
+            }
+        }
+    };
 
     // The current sub-tile: its descriptor and piece buffers, lane group
     // lg's run of contiguous pieces [j0, j1) (m pieces per run, the same for
@@ -516,18 +563,20 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         VEC % 4 == 0 && LGW_T * VEC * static_cast<int>(esz) >= 128 && (EPI & kBwdShared) == 0 ? kCpolNT : 0;
     // idle lanes: an offset past every span
     const uint32_t laneoff = c_ok ? static_cast<uint32_t>(lc) * VEC * esz : 0x80000000u;
-    // epilogue inputs of a row (sample s, local feature fl): its mask word
-    // (the one holding this lane's columns) and x; rows past a piece's end
-    // (sample NT) read zeros
+    // ReLU input of a row (sample s, local feature fl): its mask word (the
+    // one holding this lane's columns); rows past a piece's end (sample NT)
+    // read zeros
     const int MW = a.MW;
     const uint32_t rowMb = static_cast<uint32_t>(F) * MW * 4;
     const uint32_t m_word_off = static_cast<uint32_t>((lcx * VEC) >> 5) * 4;
     const int m_shift = (lcx * VEC) & 31;
-    // Lane groups of four or more lanes fetch a piece's epilogue inputs once
-    // per quad of lanes: lane lc takes row lc & 3, then each row's values
-    // are broadcast across the quad (DPP), instead of every lane loading all
+    // Lane groups of four or more lanes fetch a piece's ReLU mask words once
+    // per quad of lanes: lane lc takes row lc & 3, then each row's word is
+    // broadcast across the quad (DPP), instead of every lane loading all
     // four rows.  A quad's 4 * VEC columns lie in one mask word (VEC divides
-    // 8), the word of the quad's first lane, which idle lanes take too.
+    // 8), the word of the quad's first lane, which idle lanes take too.  (x of
+    // a row, for linear0, comes with the sort: the ranked pairs' x go to LDS
+    // in sorted order.)
     constexpr bool kQuadEpi = LGW_T >= 4;
     const int q_row = lc & 3;
     const uint32_t m_word_q =
@@ -536,7 +585,7 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     const uint32_t *t_piece = s_piece;
     int64_t sub = 0;
     int ns = 0, m = 0, j0 = 0, j1 = 0;
-    __amdgpu_buffer_rsrc_t grs = make_rsrc(a.g, 0u), mrs = grs, xrs = grs;
+    __amdgpu_buffer_rsrc_t grs = make_rsrc(a.g, 0u), mrs = grs;
     // sub-tile t, staged in LDS buffer b, becomes the current one
     auto set_tile = [&](int t, int b) __attribute__((always_inline)) {
         t_desc = s_sdesc + b * (kP + 1);
@@ -555,7 +604,6 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         grs = make_rsrc(static_cast<const char *>(a.g) + row0 * static_cast<int64_t>(D) * esz,
                         static_cast<uint32_t>(ns) * rowFb);
         if constexpr (kRelu) mrs = make_rsrc(a.mask + row0 * MW, static_cast<uint32_t>(ns) * F * MW * 4);
-        if constexpr (kLin) xrs = make_rsrc(a.x + row0, static_cast<uint32_t>(ns) * F * 4);
     };
     // Piece tt of the current sub-tile's run: its entry, its rows'
     // descriptors, and loads of their gradient rows.  Past j1 the piece is
@@ -575,7 +623,7 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         // (the 24-bit products ignore the feature bits of .y)
 #pragma unroll
         for (int i = 0; i < kL; ++i) load_grad_words<GD, VEC, kGCpol>(grs, __umul24(dv[i].y, rowFb) + flb, gv[i]);
-        if constexpr (kQuadEpi && (kRelu || kLin)) {
+        if constexpr (kQuadEpi && kRelu) {
             // this lane's row of the quad (selects on named values: indexing
             // the descriptor array would put it in scratch memory)
             const uint32_t y0 = dv[0].y, y1 = dv[1].y, y2 = dv[2].y, y3 = dv[3].y;
@@ -583,9 +631,6 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
             if constexpr (kRelu)
                 mv[0] = __builtin_amdgcn_raw_buffer_load_b32(
                     mrs, __umul24(yq, rowMb) + flp * static_cast<uint32_t>(MW) * 4 + m_word_q, 0, 0);
-            if constexpr (kLin)
-                xv[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                    xrs, __umul24(yq, static_cast<uint32_t>(F) * 4) + flp * 4, 0, 0));
         } else {
             if constexpr (kRelu) {
 #pragma unroll
@@ -593,12 +638,7 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
                     mv[i] = __builtin_amdgcn_raw_buffer_load_b32(
                         mrs, __umul24(dv[i].y, rowMb) + flp * static_cast<uint32_t>(MW) * 4 + m_word_off, 0, 0);
             }
-            if constexpr (kLin) {
-#pragma unroll
-                for (int i = 0; i < kL; ++i)
-                    xv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                        xrs, __umul24(dv[i].y, static_cast<uint32_t>(F) * 4) + flp * 4, 0, 0));
-            }
+
         }
     };
 
@@ -619,7 +659,15 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         float wk[VEC], lw[VEC], wp[VEC];
         lds_load_vec<VEC>(s_qw + __umul24(rowbase + k, D) + lcx * VEC, wk);
         if constexpr (kLin) lds_load_vec<VEC>(s_lw + __umul24(fl, D) + lcx * VEC, lw);
-        float ab[VEC], aw[VEC], ad[VEC], ax[VEC];
+        float ab[VEC], aw[VEC];
+        if constexpr (kFeatSums) {
+            if (n > 0 && fl != cur_fl) {
+                flush_feat();
+                cur_fl = fl;
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) ad_run[q] = ax_run[q] = 0.0f;
+            }
+        }
         // The piece's sums are added into LDS (a read-modify-write: this
         // lane group owns the cells): the run's first key (feature) into its
         // record, any other key (feature) into the histogram (bias sums).
@@ -659,7 +707,7 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
             float dot = 0.0f, dotl = 0.0f, dot2 = 0.0f;
             const uint32_t mvi = mask_word(i);
             float xvi = 0.0f;
-            if constexpr (kLin) xvi = kQuadEpi ? __uint_as_float(quad_bcast(__float_as_uint(xv[0]), i)) : xv[i];
+            if constexpr (kLin) xvi = s_xs[i < n ? ((pe >> 16) & 0xfff) + i : kP];
 #pragma unroll
             for (int q = 0; q < VEC; ++q) {
                 const float gm = g_masked(i, q, mvi);
@@ -667,13 +715,10 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
                 // (the first row starts the piece's sums)
                 ab[q] = i == 0 ? gq : ab[q] + gq;
                 aw[q] = i == 0 ? qf * gq : fmaf(qf, gq, aw[q]);
-                if constexpr (kRawDb) {
-                    const float gd = kLin ? grad_elem<GD>(gv[i], q) : gm;
-                    ad[q] = i == 0 ? gd : ad[q] + gd;
-                }
+                if constexpr (kRawDb) ad_run[q] += kLin ? grad_elem<GD>(gv[i], q) : gm;
                 if constexpr (kLin) {
                     const float graw = grad_elem<GD>(gv[i], q);
-                    ax[q] = i == 0 ? graw * xvi : fmaf(graw, xvi, ax[q]);
+                    ax_run[q] = fmaf(graw, xvi, ax_run[q]);
                     dotl = fmaf(graw, lw[q], dotl);
                 }
                 dot = fmaf(gq, wk[q], dot);
@@ -711,25 +756,6 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
             }
             lds_store_vec<VEC>(dst, hb);
             lds_store_vec<VEC>(dst + D, hw);
-            if constexpr (kRawDb) {
-                // (the per-feature sums of the epilogue kernels: read here,
-                // not ahead, to keep their registers down)
-                const bool first = fl == fl0;
-                float *dstd = first ? rec + D2 : s_db + __umul24(fl, D) + lc * VEC;
-                float hd[VEC];
-                lds_load_vec<VEC>(dstd, hd);
-#pragma unroll
-                for (int q = 0; q < VEC; ++q) hd[q] += ad[q];
-                lds_store_vec<VEC>(dstd, hd);
-                if constexpr (kLin) {
-                    float *dstx = first ? rec + D2 + D : s_dlw + __umul24(fl, D) + lc * VEC;
-                    float hx[VEC];
-                    lds_load_vec<VEC>(dstx, hx);
-#pragma unroll
-                    for (int q = 0; q < VEC; ++q) hx[q] += ax[q];
-                    lds_store_vec<VEC>(dstx, hx);
-                }
-            }
         }
         // dx into the rows' descriptors (rows past the piece's end: the
         // discard slot)
@@ -795,6 +821,10 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         const bool more = t + 1 < t_end;
         if (more) {
             tile_rank<Q, RB>(a, t + 1, nfh, tid, pk, pv, s_nb, s_edge, s_iw, s_cnt, ko, qb);
+            if constexpr (kLin) {
+#pragma unroll
+                for (int u = 0; u < kP / RB; ++u) xk[u] = pv[u];
+            }
             if (t + 2 < t_end) load_pairs(t + 2);
         }
 
@@ -810,8 +840,9 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         }
         if (lc == 0) {
             s_rkey[lg] = key0;
-            if constexpr (kRawDb) s_rfl[lg] = fl0;
+            if constexpr (kFeatSums) s_rfl[lg] = fl0;
         }
+        cur_fl = -1;
         if (m > 0) {
             int tt = 0;
 #pragma unroll 1
@@ -826,6 +857,7 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
             if (tt < m) process(tt, gA, dA, pA, mA, xA);
             if (tt + 1 < m) process(tt + 1, gB, dB, pB, mB, xB);
         }
+        flush_feat();
         __syncthreads();
         const int64_t h_sub = sub;
         const int h_ns = ns;
@@ -876,22 +908,22 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
                     h[D + q] += sw[q];
                 }
             }
-            const int rfl = kRawDb ? s_rfl[lg] : -1;
-            if (kRawDb && rfl >= 0 && (lg == 0 || s_rfl[lg - 1] != rfl)) {
+            const int rfl = kFeatSums ? s_rfl[lg] : -1;
+            if (kFeatSums && rfl >= 0 && (lg == 0 || s_rfl[lg - 1] != rfl)) {
                 float sd[VEC], sx[VEC];
 #pragma unroll
                 for (int q = 0; q < VEC; ++q) sd[q] = sx[q] = 0.0f;
                 for (int j = lg; j < LG && s_rfl[j] == rfl; ++j) {
-                    const float *rj = s_rec + j * RS + D2 + lc * VEC;
+                    const float *rj = s_rec + j * RS + lc * VEC;
 #pragma unroll
                     for (int q = 0; q < VEC; ++q) {
-                        sd[q] += rj[q];
-                        if constexpr (kLin) sx[q] += rj[D + q];
+                        if constexpr (kRawDb) sd[q] += rj[D2 + q];
+                        if constexpr (kLin) sx[q] += rj[off_ax + q];
                     }
                 }
 #pragma unroll
                 for (int q = 0; q < VEC; ++q) {
-                    s_db[rfl * D + lc * VEC + q] += sd[q];
+                    if constexpr (kRawDb) s_db[rfl * D + lc * VEC + q] += sd[q];
                     if constexpr (kLin) s_dlw[rfl * D + lc * VEC + q] += sx[q];
                 }
             }
@@ -899,7 +931,7 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         // S. the placing part of the next sub-tile's sort (its first barrier
         //    also orders the record reads above before the next sub-tile's
         //    record writes)
-        if (more) tile_place<RB>(a, tid, ko, qb, s_cnt, s_seg, s_tmp, s_sdesc, s_piece, s_npc);
+        if (more) tile_place<RB, kLin>(a, tid, ko, qb, s_cnt, s_seg, s_tmp, s_sdesc, s_piece, s_npc, xk, s_xs);
         // this barrier orders the histogram updates before the next
         // sub-tile's pieces, the sort's descriptors before they are read, and
         // the count reads before the next ranking zeroes them
@@ -1249,10 +1281,11 @@ size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_
     take(g.ro_npc, bufs * 4ull);
     take(g.ro_rec, (8ull + (raw_db ? 4ull : 0ull) + (lin ? 4ull : 0ull)) * LG * D);
     take(g.ro_rkey, 4ull * LG);
-    take(g.ro_rfl, raw_db ? 4ull * LG : 0ull);
+    take(g.ro_rfl, raw_db || lin ? 4ull * LG : 0ull);
     take(g.ro_dx, FS > 1 ? 4ull * (kP + 1) : 0ull);
     take(g.ro_lw, lin ? 4ull * FS * D : 0ull);
     take(g.ro_dlw, lin ? 4ull * FS * D : 0ull);
+    take(g.ro_xs, lin ? 4ull * (kP + 1) : 0ull);
     take(g.ro_edge, 4ull * FS * (B + 1));
     take(g.ro_cnt, 2ull * kBlocks * cnt_stride(NK));
     take(g.ro_seg, 4ull * (NK + 1));
@@ -1326,7 +1359,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                 // linear0 branch): c2 -20 us; where two fit, the wide form
                 // measured slower (c3 +28 us, c4 +190 us).
                 {
-                    const bool wide_ok = !raw_db && !g16;
+                    const bool wide_ok = !raw_db && !g16 && !lin;
                     bool wide = wide_ok && kLdsMax / best_lds < 2;
                     const int rb_env = tuning(PLE_TUNE_BWD_RB);
                     if (rb_env == kBlock || rb_env == kWideBlock) wide = wide_ok && rb_env == kWideBlock;
@@ -1558,7 +1591,8 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
     hipError_t e = hipSuccess;
     const int epi = (a.mask ? kBwdRelu : 0) | (a.lin_w ? kBwdLin : 0);
     if (pl.sorted) {
-        a.db_from_buckets = (Q == PLE_DTYPE_F32 || GD == Q) && a.lin_w == nullptr;
+        // (linear0's bias gradient without a ReLU: the buckets sum the unmasked g)
+        a.db_from_buckets = (Q == PLE_DTYPE_F32 || GD == Q) && (a.lin_w == nullptr || a.mask == nullptr);
         const dim3 grid(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, pl.C)));
         a.idxb = idxb;
         // one chunk: the gradient kernel writes dW / db itself
@@ -1667,7 +1701,7 @@ size_t backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D) {
     for (int al = 0; al < 2; ++al)
         for (int g16 = 0; g16 < 2; ++g16)
             for (int raw = 0; raw < 2; ++raw)
-                for (int lin = 0; lin <= raw; ++lin) {
+                for (int lin = 0; lin < 2; ++lin) {
                     const size_t t = plan_backward(N, F, B, D, al != 0, g16 != 0, raw != 0, lin != 0).total();
                     need = t > need ? t : need;
                 }
@@ -1678,7 +1712,7 @@ size_t backward_workspace_bytes(int64_t N, int64_t F, int64_t B, int64_t D) {
 
 int backward_plan_info(const BackwardRequest &r, ple_backward_plan_info_t *info) {
     const bool lin = r.lin_w != nullptr;
-    const bool raw_db = (r.quant != PLE_DTYPE_F32 && r.quant != r.grad_dtype) || lin;
+    const bool raw_db = (r.quant != PLE_DTYPE_F32 && r.quant != r.grad_dtype) || (lin && r.relu);
     const uintptr_t gaddr = reinterpret_cast<uintptr_t>(r.g);
     const BwdPlan &pl = plan_cached(r.N, r.F, r.B, r.D, gaddr % 16 == 0, r.grad_dtype != PLE_DTYPE_F32, raw_db, lin);
     info->sorted = pl.sorted ? 1 : 0;
@@ -1709,7 +1743,7 @@ int backward_run(const BackwardRequest &r) {
     if (gaddr % gbytes != 0) return PLE_E_MISALIGNED;
     // (a gradient in the quantisation dtype is its own rounding: its bias
     // gradient is the sum of the buckets, as for fp32)
-    const bool raw_db = (r.quant != PLE_DTYPE_F32 && r.quant != r.grad_dtype) || lin;
+    const bool raw_db = (r.quant != PLE_DTYPE_F32 && r.quant != r.grad_dtype) || (lin && r.relu);
     const BwdPlan &pl = plan_cached(r.N, r.F, r.B, r.D, gaddr % 16 == 0, r.grad_dtype != PLE_DTYPE_F32, raw_db, lin);
     // The workspace holds chunk partials of dW / db only (the sorted path's
     // descriptors live in LDS): dx alone needs none.
