@@ -169,6 +169,10 @@ int ple_backward_launch_noalloc(const void *grad_output, const float *x, const f
  *   lds_bytes          gradient-kernel LDS per workgroup
  *   workspace_bytes    workspace a launch that writes grad_weight / grad_bias
  *                      needs (0 for grad_x alone)
+ *   bins_per_window    bins whose tables and histogram cells a workgroup holds
+ *                      in LDS (sorted path; B when all of them fit)
+ *   windows            workgroups per feature group, one per window of bins
+ *                      (sorted path; 1 when all bins fit)
  */
 typedef struct ple_backward_plan_info {
     int sorted;
@@ -179,6 +183,8 @@ typedef struct ple_backward_plan_info {
     int threads;
     size_t lds_bytes;
     size_t workspace_bytes;
+    int bins_per_window;
+    int windows;
 } ple_backward_plan_info_t;
 int ple_backward_plan_query(const void *grad_output, int64_t N, int64_t F, int64_t B, int64_t D,
                             int grad_dtype, int quant_dtype, int relu, int linear0,

@@ -55,6 +55,8 @@ class BackwardPlanInfo(ctypes.Structure):
         ("threads", ctypes.c_int),
         ("lds_bytes", ctypes.c_size_t),
         ("workspace_bytes", ctypes.c_size_t),
+        ("bins_per_window", ctypes.c_int),
+        ("windows", ctypes.c_int),
     ]
 
 

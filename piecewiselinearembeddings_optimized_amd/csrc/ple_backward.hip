@@ -85,9 +85,14 @@ struct BwdArgs {
     int fin_direct;        // finalize: chunk sums read straight from the partials (no LDS table)
     int fin_summed;        // finalize: the chunk partials are summed into chunk 0 already
     int fin_fused;         // sorted path, one chunk: dW / db straight from the LDS histogram (no finalize kernel)
-    int idxb;              // bytes per bin index (1 or 2 on the sorted path)
+    int idxb;              // bytes per bin index
     // sorted path
     int FS, G, NT, T, SPC, PM, LGW;   // T sub-tiles, SPC sub-tiles per chunk, PM piece capacity
+    // Bin windows: a workgroup holds the tables and histogram cells of BW
+    // consecutive bins of its features (BW = B, NW = 1 when every bin fits
+    // in LDS); the NW windows of a feature group are NW workgroups, and
+    // each pair is reduced (and its dx written) by the window of its bin.
+    int BW, NW;
     int ro_qw, ro_hist, ro_db, ro_iw, ro_nb, ro_desc, ro_piece, ro_npc, ro_rec, ro_rkey, ro_rfl, ro_dx,
         ro_lw, ro_dlw, ro_xs, ro_edge, ro_cnt, ro_seg, ro_tmp;   // fused kernel LDS (ro_dx < 0: no dx staging)
 };
@@ -208,12 +213,12 @@ __device__ __forceinline__ void tile_load(const BwdArgs &a, int t, int f0, int n
 // read, and between this sort's part B / C and the next sort's part A (one
 // count buffer).
 template <int Q, int RB>
-__device__ __forceinline__ void tile_rank(const BwdArgs &a, int t, int nfh, int tid, const int (&pk)[kP / RB],
+__device__ __forceinline__ void tile_rank(const BwdArgs &a, int t, int k0, int nfh, int tid, const int (&pk)[kP / RB],
                                           const float (&pv)[kP / RB], const int *s_nb, const float *s_edge,
                                           const float *s_iw, uint16_t *s_cnt, int (&ko)[kP / RB],
                                           uint32_t (&qb)[kP / RB]) {
     constexpr int kPR = kP / RB;
-    const int FS = a.FS, B = a.B, NT = a.NT;
+    const int FS = a.FS, B = a.BW, NT = a.NT;    // (B: the window's bins)
     const int fs_shift = __ffs(FS) - 1;
     const int ns = static_cast<int>(min(static_cast<int64_t>(NT), a.N - static_cast<int64_t>(t) * NT));
     const int NK = FS * B;                       // keys; NK marks padding
@@ -231,8 +236,8 @@ __device__ __forceinline__ void tile_rank(const BwdArgs &a, int t, int nfh, int 
             if ((1 << i) < FS) flm &= ((fl >> i) & 1) ? kPat[i] : ~kPat[i];
     }
     const int n = s_nb[fl];
-    const float *erow = s_edge + fl * (B + 1);
-    const float *irow = s_iw + fl * B;
+    const float *erow = s_edge + fl * (B + 1);   // edges k0 .. k0 + B
+    const float *irow = s_iw + fl * B;           // inverse widths of bins k0 .. k0 + B - 1
     const unsigned long long lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
     // Each block's count row belongs to the one wave that ranks the block:
     // that wave zeroes the row first (its own stores stay in order, and the
@@ -249,14 +254,16 @@ __device__ __forceinline__ void tile_rank(const BwdArgs &a, int t, int nfh, int 
     for (int u = 0; u < kPR; ++u) {
         const int p = tid + u * RB;
         const int s = p >> fs_shift;
-        const bool valid = f_ok && s < ns;
-        const int k = clamp_bin(pk[u], n);
+        const int kg = clamp_bin(pk[u], n);     // the pair's bin; its place in the window:
+        const bool inw = static_cast<unsigned>(kg - k0) < static_cast<unsigned>(B);
+        const int k = inw ? kg - k0 : 0;
+        const bool valid = f_ok && s < ns && inw;
         const float v = pv[u];
         const float e = erow[k];
         const uint32_t q = __float_as_uint(quant<Q>((v - e) * irow[k]));
         // x on e_k (k >= 1) gives q(frac) == +0 exactly; such rows carry -0
         // instead, which marks the edge term and adds the same zero
-        qb[u] = (k > 0 && v == e) ? 0x80000000u : (q == 0x80000000u ? 0u : q);
+        qb[u] = (kg > 0 && v == e) ? 0x80000000u : (q == 0x80000000u ? 0u : q);
         const int kk = valid ? k : B;
         unsigned long long m = flm;
         for (int bit = 0; bit < kb; ++bit) {
@@ -279,7 +286,7 @@ __device__ __forceinline__ void tile_place(const BwdArgs &a, int tid, const int 
                                            uint2 *desc, uint32_t *piece, int *npc, const float (&xk)[kP / RB],
                                            float *xs) {
     constexpr int kPR = kP / RB;
-    const int FS = a.FS, B = a.B;
+    const int FS = a.FS, B = a.BW;
     const int fs_shift = __ffs(FS) - 1;
     const int NK = FS * B;
     const int lane = tid & (kWave - 1);
@@ -379,8 +386,9 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     constexpr bool kRawDb = !kGradExact || (kLin && kRelu);
     constexpr bool kFeatSums = kRawDb || kLin;
     extern __shared__ __align__(16) unsigned char lds[];
-    const int FS = a.FS, B = a.B, D = a.D, F = a.F, NT = a.NT;
-    float *s_qw = reinterpret_cast<float *>(lds + a.ro_qw);             // [FS][B][D] q(W) * iw
+    // B: the bins of a window (the LDS tables' and the keys' width); Bg: of the weight
+    const int FS = a.FS, B = a.BW, D = a.D, F = a.F, NT = a.NT, Bg = a.B;
+    float *s_qw = reinterpret_cast<float *>(lds + a.ro_qw);             // [FS][B+1][D] q(W) * iw, bins k0-1 ..
     float *s_hist = reinterpret_cast<float *>(lds + a.ro_hist);         // [FS][B][2D]
     float *s_db = reinterpret_cast<float *>(lds + a.ro_db);             // [FS][D]
     float *s_iw = reinterpret_cast<float *>(lds + a.ro_iw);             // [FS][B]
@@ -404,6 +412,10 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
 
     int g, c;
     if (!decode_tile(blockIdx.x, a.G, a.C, g, c)) return;
+    // (the windows of a feature group are neighbours: they share its chunk's
+    // bin indices and x in the L2)
+    const int k0 = (g % a.NW) * B;   // the window's first bin
+    g /= a.NW;
     const int f0 = g * FS;
     const int nfh = min(FS, F - f0);
     const int t_begin = c * a.SPC;
@@ -413,12 +425,13 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     const int PM = a.PM;
 
     // the sort's pairs of the next sub-tile (bin index, x), loaded a sub-tile
-    // ahead; bin indices are uint8 or int16 here (at most 4096 bins)
+    // ahead
     int pk[kP / RB];
     float pv[kP / RB];
     auto load_pairs = [&](int t) __attribute__((always_inline)) {
         if (a.idxb == 1) tile_load<RB, uint8_t>(a, t, f0, nfh, tid, pk, pv);
-        else tile_load<RB, int16_t>(a, t, f0, nfh, tid, pk, pv);
+        else if (a.idxb == 2) tile_load<RB, int16_t>(a, t, f0, nfh, tid, pk, pv);
+        else tile_load<RB, int32_t>(a, t, f0, nfh, tid, pk, pv);
     };
     load_pairs(t_begin);
     int ko[kP / RB];          // the next sub-tile's keys | ranks, and q(frac) bits
@@ -432,14 +445,19 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     if constexpr (kLin) {
         if (tid == 0) s_xs[kP] = 0.0f;   // (rows past a piece's end)
     }
-    for (int i = tid; i < FS; i += NTH) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], B) : 1;
+    for (int i = tid; i < FS; i += NTH) s_nb[i] = i < nfh ? clamp_nbins(a.nbins[f0 + i], Bg) : 1;
+    // (the window's inverse widths and edges; rows past the last feature are
+    // never read: their pairs are padding)
     for (int i = tid; i < FS * B; i += NTH) {
         const int fl = i / B;
-        s_iw[i] = fl < nfh ? a.iw[static_cast<int64_t>(f0) * B + i] : 0.0f;
+        const int kg = k0 + i - fl * B;
+        s_iw[i] = fl < nfh && kg < Bg ? a.iw[static_cast<int64_t>(f0 + fl) * Bg + kg] : 0.0f;
     }
-    // (rows past the last feature are never read: their pairs are padding)
-    for (int i = tid; i < FS * (B + 1); i += NTH)
-        s_edge[i] = i < nfh * (B + 1) ? a.edges[static_cast<int64_t>(f0) * (B + 1) + i] : 0.0f;
+    for (int i = tid; i < FS * (B + 1); i += NTH) {
+        const int fl = i / (B + 1);
+        const int kg = k0 + i - fl * (B + 1);
+        s_edge[i] = fl < nfh && kg <= Bg ? a.edges[static_cast<int64_t>(f0 + fl) * (Bg + 1) + kg] : 0.0f;
+    }
     for (int i = tid; i < FS * B * 2 * D; i += NTH) s_hist[i] = 0.0f;
     for (int i = tid; i < FS * D; i += NTH) s_db[i] = 0.0f;
     if constexpr (kLin) {
@@ -450,25 +468,29 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     }
     __syncthreads();
     // the weight rows pre-scaled by their bin's inverse width: a row's dx term
-    // iw_k <g, q(W[phys k])> is then one dot product with the table row
-    for (int i = tid; i < FS * B * D; i += NTH) {
-        const int fl = i / (B * D);
-        const int r = i - fl * (B * D);
-        const int k = r / D;
-        const int j = r - k * D;
+    // iw_k <g, q(W[phys k])> is then one dot product with the table row.
+    // Row r of a feature holds bin k0 + r - 1 (row 0: the bin below the
+    // window, for the edge term of the window's first bin; zeros below bin 0).
+    for (int i = tid; i < FS * (B + 1) * D; i += NTH) {
+        const int fl = i / ((B + 1) * D);
+        const int r = i - fl * ((B + 1) * D);
+        const int rr = r / D;
+        const int j = r - rr * D;
+        const int kg = k0 + rr - 1;
         float w = 0.0f;
         if (fl < nfh) {
             const int n = s_nb[fl];
-            if (k < n)
-                w = quant<Q>(a.weight[(static_cast<int64_t>(f0 + fl) * B + phys_bin(k, n, B)) * D + j]) *
-                    s_iw[fl * B + k];
+            if (kg >= 0 && kg < n) {
+                const int64_t fr = static_cast<int64_t>(f0 + fl) * Bg;
+                w = quant<Q>(a.weight[(fr + phys_bin(kg, n, Bg)) * D + j]) * a.iw[fr + kg];
+            }
         }
         s_qw[i] = w;
     }
 
     // the first sub-tile's sort (the tables it reads are staged before the
     // barrier above), then the next sub-tile's pairs
-    tile_rank<Q, RB>(a, t_begin, nfh, tid, pk, pv, s_nb, s_edge, s_iw, s_cnt, ko, qb);
+    tile_rank<Q, RB>(a, t_begin, k0, nfh, tid, pk, pv, s_nb, s_edge, s_iw, s_cnt, ko, qb);
 #pragma unroll
     for (int u = 0; u < kP / RB; ++u) xk[u] = kLin ? pv[u] : 0.0f;
     __syncthreads();
@@ -656,8 +678,10 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         const int fl = key >> 12;
         const int k = key & 0xfff;
         const int rowbase = __umul24(fl, B);
+        // (table row of bin k: k + 1; of the bin below, for the edge term: k)
+        const int qrow = __umul24(fl, B + 1) + k;
         float wk[VEC], lw[VEC], wp[VEC];
-        lds_load_vec<VEC>(s_qw + __umul24(rowbase + k, D) + lcx * VEC, wk);
+        lds_load_vec<VEC>(s_qw + __umul24(qrow + 1, D) + lcx * VEC, wk);
         if constexpr (kLin) lds_load_vec<VEC>(s_lw + __umul24(fl, D) + lcx * VEC, lw);
         float ab[VEC], aw[VEC];
         if constexpr (kFeatSums) {
@@ -698,7 +722,7 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         // epilogues' kernels fold it into the first pass (a second pass
         // there takes them past 256 VGPRs, one wave per SIMD).
         constexpr bool kEdgePass = !kRelu && !kLin;
-        if constexpr (!kEdgePass) lds_load_vec<VEC>(s_qw + __umul24(rowbase + (k > 0 ? k - 1 : 0), D) + lcx * VEC, wp);
+        if constexpr (!kEdgePass) lds_load_vec<VEC>(s_qw + __umul24(qrow, D) + lcx * VEC, wp);
         float parts[kL];
         bool edge = false;
 #pragma unroll
@@ -735,7 +759,7 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
         // Edge rows are rare in most data: the wave takes this branch only
         // when one of its lane groups holds one.
         if (kEdgePass && __any(edge)) {
-            lds_load_vec<VEC>(s_qw + __umul24(rowbase + (k > 0 ? k - 1 : 0), D) + lcx * VEC, wp);
+            lds_load_vec<VEC>(s_qw + __umul24(qrow, D) + lcx * VEC, wp);
 #pragma unroll
             for (int i = 0; i < kL; ++i) {
                 const uint32_t mvi = mask_word(i);
@@ -820,7 +844,7 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
     for (int t = t_begin; t < t_end; ++t) {
         const bool more = t + 1 < t_end;
         if (more) {
-            tile_rank<Q, RB>(a, t + 1, nfh, tid, pk, pv, s_nb, s_edge, s_iw, s_cnt, ko, qb);
+            tile_rank<Q, RB>(a, t + 1, k0, nfh, tid, pk, pv, s_nb, s_edge, s_iw, s_cnt, ko, qb);
             if constexpr (kLin) {
 #pragma unroll
                 for (int u = 0; u < kP / RB; ++u) xk[u] = pv[u];
@@ -875,7 +899,8 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
                 if (fl < nfh && sidx < h_ns) a.dx[(h_sub + sidx) * F + f0 + fl] = s_dx[p];
             }
         } else if (a.dx) {
-            const int rows = h_ns * nfh;
+            // (the sub-tile's sorted rows: its pairs in this window)
+            const int rows = s_seg[FS * B] & 0xffff;
 #pragma unroll
             for (int u = 0; u < (kP / RB); ++u) {
                 const int j = tid + u * RB;
@@ -956,10 +981,11 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
             const int fl = ok ? col / D : 0;
             const int j = ok ? col - fl * D : 0;
             const int n = ok ? s_nb[fl] : 0;
+            // (one window: B == Bg)
             const float *h = s_hist + static_cast<size_t>(fl) * B * D2 + j;   // bucket at k * D2, weighted at + D
             auto total = [&](int k, int hh) __attribute__((always_inline)) { return h[k * D2 + hh * D]; };
-            float *dwc = ok && a.dw ? a.dw + static_cast<int64_t>(f0 + fl) * B * D + j : nullptr;
-            const float incl = dw_suffix(total, n, B, D, l, dwc);
+            float *dwc = ok && a.dw ? a.dw + static_cast<int64_t>(f0 + fl) * Bg * D + j : nullptr;
+            const float incl = dw_suffix(total, n, Bg, D, l, dwc);
             if (ok && l == 0) {
                 const int64_t fj = static_cast<int64_t>(f0 + fl) * D + j;
                 if (a.db) a.db[fj] = a.db_from_buckets ? incl : s_db[fl * D + j];
@@ -973,12 +999,13 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
 
     // chunk partials
     if (a.part) {
+        // (the window's cells: bins k0 .. k0 + B - 1 of the partials' Bg)
         const int D2 = 2 * D;
-        float *dst = a.part + (static_cast<int64_t>(c) * F + f0) * B * D2;
+        float *dst = a.part + (static_cast<int64_t>(c) * F + f0) * Bg * D2 + static_cast<int64_t>(k0) * D2;
         for (int i = tid; i < FS * B * D2; i += NTH) {
             const int fl = i / (B * D2);
-            const int k = (i - fl * B * D2) / D2;
-            if (fl < nfh && k < s_nb[fl]) dst[i] = s_hist[i];
+            const int r = i - fl * B * D2;
+            if (fl < nfh && k0 + r / D2 < s_nb[fl]) dst[static_cast<int64_t>(fl) * Bg * D2 + r] = s_hist[i];
         }
         if constexpr (kRawDb) {
             float *dstb = a.part_db + (static_cast<int64_t>(c) * F + f0) * D;
@@ -1264,14 +1291,14 @@ struct LdsTaker {
     }
 };
 
-// raw_db: records carry the raw-gradient bias sums too (quantised gradients,
-// linear0 epilogue); lin: and the linear0 weight sums.  The sort's edges,
-// block counts, key starts and wave totals.
+// B: the bins of a window.  raw_db: records carry the raw-gradient bias sums
+// too (quantised gradients, linear0 epilogue); lin: and the linear0 weight
+// sums.  The sort's edges, block counts, key starts and wave totals.
 size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_db, bool lin) {
     constexpr int bufs = 1;
     const int NK = FS * B;
     LdsTaker take;
-    take(g.ro_qw, 4ull * FS * B * D);
+    take(g.ro_qw, 4ull * FS * (B + 1) * D);
     take(g.ro_hist, 8ull * FS * B * D);
     take(g.ro_db, 4ull * FS * D);
     take(g.ro_iw, 4ull * FS * B);
@@ -1302,9 +1329,10 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
     pl.rb = kBlock;
     const int cus = device_cu_count();
     pl.sorted = false;
-    // Sorted path: bins fit the 12-bit field of a piece, and a sub-tile's
-    // gradient rows span less than 2^31 bytes (32-bit buffer offsets).
-    if (B <= 4096 && static_cast<int64_t>(kP) * F * D * 4 < INT32_MAX && tuning(PLE_TUNE_BWD_SIMPLE) == 0) {
+    // Sorted path: a sub-tile's gradient rows span less than 2^31 bytes
+    // (32-bit buffer offsets); the bins of a workgroup fit the 12-bit field of
+    // a piece -- all of them, or a window of them.
+    if (static_cast<int64_t>(kP) * F * D * 4 < INT32_MAX && tuning(PLE_TUNE_BWD_SIMPLE) == 0) {
         // 4 floats per lane (16-byte loads for fp32 gradients) when D allows
         // (8 a lane halved the per-row instructions but needed registers for
         // two waves per SIMD only, and hid less latency); lane groups of a
@@ -1328,11 +1356,12 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
             int best_fs = 0;
             size_t best_lds = 0;
             BwdArgs geo{};
-            auto pm_for = [&](int fs) { return kP / kL + static_cast<int>(std::min<int64_t>(kP, fs * B)); };
-            for (int fs = 4; fs >= 1; fs /= 2) {
+            auto pm_for = [&](int fs, int64_t bw) { return kP / kL + static_cast<int>(std::min<int64_t>(kP, fs * bw)); };
+            int bw = static_cast<int>(std::min<int64_t>(B, 4096)), nw = 1;
+            for (int fs = 4; fs >= 1 && B <= 4096; fs /= 2) {
                 if ((fs > 1 && fs > F) || static_cast<int64_t>(fs) * B >= 65536) continue;
                 BwdArgs t{};
-                const size_t lds = reduce_layout(t, fs, static_cast<int>(B), static_cast<int>(D), LG, pm_for(fs), raw_db, lin);
+                const size_t lds = reduce_layout(t, fs, static_cast<int>(B), static_cast<int>(D), LG, pm_for(fs, B), raw_db, lin);
                 if (lds <= kReduceLdsTarget || (fs == 1 && lds <= kLdsMax)) {
                     best_fs = fs;
                     best_lds = lds;
@@ -1341,19 +1370,45 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                 }
             }
             const int fs_env = tuning(PLE_TUNE_BWD_FS);
-            if ((fs_env == 1 || fs_env == 2 || fs_env == 4 || fs_env == 8 || fs_env == 16) &&
+            if ((fs_env == 1 || fs_env == 2 || fs_env == 4 || fs_env == 8 || fs_env == 16) && B <= 4096 &&
                 static_cast<int64_t>(fs_env) * B < 65536) {
                 BwdArgs t{};
-                const size_t lds = reduce_layout(t, fs_env, static_cast<int>(B), static_cast<int>(D), LG, pm_for(fs_env), raw_db, lin);
+                const size_t lds = reduce_layout(t, fs_env, static_cast<int>(B), static_cast<int>(D), LG, pm_for(fs_env, B), raw_db, lin);
                 if (lds <= kLdsMax) {
                     best_fs = fs_env;
                     best_lds = lds;
                     geo = t;
                 }
             }
+            // Tables beyond LDS (or beyond 4096 bins): windows of bins, one
+            // feature a workgroup, as wide as two workgroups per CU allow,
+            // then evened out over the bins.  Every window ranks all pairs
+            // of its sub-tiles and reduces those of its bins, so the gradient
+            // is still read once; the bin indices and x once per window.
+            // Windows split a feature's per-feature sums (raw-gradient bias,
+            // linear0), so those plans keep the fallback kernels.
+            if (best_fs == 0 && !raw_db && !lin) {
+                auto lds_of = [&](BwdArgs &t, int w) {
+                    return reduce_layout(t, 1, w, static_cast<int>(D), LG, pm_for(1, w), raw_db, lin);
+                };
+                int lo = 1, hi = static_cast<int>(std::min<int64_t>(B, 4096));
+                BwdArgs t{};
+                if (lds_of(t, lo) <= kReduceLdsTarget) {
+                    while (lo < hi) {   // the widest window within the target
+                        const int mid = (lo + hi + 1) / 2;
+                        if (lds_of(t, mid) <= kReduceLdsTarget) lo = mid;
+                        else hi = mid - 1;
+                    }
+                    nw = static_cast<int>((B + lo - 1) / lo);
+                    bw = static_cast<int>((B + nw - 1) / nw);
+                    best_fs = 1;
+                    best_lds = lds_of(t, bw);
+                    geo = t;
+                }
+            }
             int rb = kBlock;
             if (best_fs > 0) {
-                const int PM = pm_for(best_fs);
+                const int PM = pm_for(best_fs, nw > 1 ? bw : B);
                 // Twice the workgroup size where LDS leaves room for one
                 // reduce workgroup per CU (fp32 gradient and quantisation, no
                 // linear0 branch): c2 -20 us; where two fit, the wide form
@@ -1365,8 +1420,8 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                     if (rb_env == kBlock || rb_env == kWideBlock) wide = wide_ok && rb_env == kWideBlock;
                     if (wide) {
                         BwdArgs tw = geo;
-                        const size_t ldsw = reduce_layout(tw, best_fs, static_cast<int>(B), static_cast<int>(D),
-                                                          kWideBlock / lgw, PM, raw_db, lin);
+                        const size_t ldsw = reduce_layout(tw, best_fs, nw > 1 ? bw : static_cast<int>(B),
+                                                          static_cast<int>(D), kWideBlock / lgw, PM, raw_db, lin);
                         if (ldsw <= kLdsMax) {
                             geo = tw;
                             best_lds = ldsw;
@@ -1380,7 +1435,9 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
                     pl.rb = rb;
                     pl.lds = best_lds;
                     geo.FS = best_fs;
-                    geo.G = static_cast<int>((F + best_fs - 1) / best_fs);
+                    geo.BW = nw > 1 ? bw : static_cast<int>(B);
+                    geo.NW = nw;
+                    geo.G = static_cast<int>((F + best_fs - 1) / best_fs) * nw;
                     geo.NT = kP / best_fs;
                     geo.T = static_cast<int>((N + geo.NT - 1) / geo.NT);
                     geo.PM = PM;
@@ -1426,9 +1483,10 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
         pl.hist_global = pl.lds > kLdsMax || tuning(PLE_TUNE_BWD_SIMPLE_GLOBAL) == 1;
         if (pl.hist_global) pl.lds = 0;
     }
-    // A sorted plan of one chunk writes dW and db from the gradient kernel's
-    // LDS histogram (no chunk partials); other plans keep per-chunk partials.
-    if (!(pl.sorted && pl.C == 1)) {
+    // A sorted plan of one chunk and one window writes dW and db from the
+    // gradient kernel's LDS histogram (no chunk partials); other plans keep
+    // per-chunk partials.
+    if (!(pl.sorted && pl.C == 1 && pl.geo.NW == 1)) {
         pl.part_bytes = static_cast<size_t>(pl.Cd) * F * B * 2 * D * sizeof(float);
         pl.part_db_bytes = static_cast<size_t>(pl.Cd) * F * D * sizeof(float);
         pl.part_lw_bytes = lin ? static_cast<size_t>(pl.Cd) * F * D * sizeof(float) : 0;
@@ -1595,8 +1653,8 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
         a.db_from_buckets = (Q == PLE_DTYPE_F32 || GD == Q) && (a.lin_w == nullptr || a.mask == nullptr);
         const dim3 grid(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, pl.C)));
         a.idxb = idxb;
-        // one chunk: the gradient kernel writes dW / db itself
-        a.fin_fused = want_dwdb && pl.C == 1;
+        // one chunk (and one window): the gradient kernel writes dW / db itself
+        a.fin_fused = want_dwdb && pl.C == 1 && a.NW == 1;
         const TimerSlot ts = timer_slot(PLE_TIMER_BACKWARD);
         t_slot = ts;
         e = launch_reduce<GD, Q>(a, pl.vec, epi, pl.rb, grid, pl.lds, s);
@@ -1723,6 +1781,8 @@ int backward_plan_info(const BackwardRequest &r, ple_backward_plan_info_t *info)
     info->threads = pl.sorted ? pl.rb : kWave;
     info->lds_bytes = pl.lds;
     info->workspace_bytes = pl.total();
+    info->bins_per_window = pl.sorted ? pl.geo.BW : static_cast<int>(r.B);
+    info->windows = pl.sorted ? pl.geo.NW : 1;
     return PLE_OK;
 }
 

@@ -122,10 +122,30 @@ def test_backward_plan_query_and_workspace_sizes():
     assert capi.workspace_bytes(65536, 128, 48, 32) >= c1["workspace_bytes"]
     c4 = capi.backward_plan(8192, 1024, 96, 24, grad_dtype=torch.bfloat16)
     assert c4["sorted"] == 1 and c4["chunks"] == 1 and c4["columns_per_lane"] == 8
-    wide = capi.backward_plan(2048, 4, 40000, 4)    # tables beyond LDS: the fallback kernels
-    assert wide["sorted"] == 0 and wide["workspace_bytes"] >= 4 * 40000 * 2 * 4 * 4
+    assert c1["windows"] == 1 and c1["bins_per_window"] == 48
     with pytest.raises(capi.PleError):
         capi.backward_plan(1024, 8, 48, 24, grad_dtype=torch.bfloat16, quant_dtype=torch.float16)
+
+
+@pytest.mark.parametrize("n,f,bmax,d", [(2048, 4, 40000, 4), (65536, 128, 1024, 32), (65536, 64, 4096, 16),
+                                        (65536, 32, 48, 256), (2048, 3, 32768, 2), (1000, 3, 700, 62)])
+def test_backward_plan_bin_windows(n, f, bmax, d):
+    """Tables beyond LDS take the sorted path in windows of bins: the
+    windows cover every bin (bins_per_window * windows >= B, no empty last
+    window), each fits the 12-bit bin field of a piece and two workgroups'
+    LDS per CU, and the partials (whole tables, every chunk) are in the
+    workspace even for one chunk.  Plans with the per-feature sums of the
+    module epilogues keep the fallback kernels."""
+    from piecewiselinearembeddings_optimized_amd import capi
+
+    pl = capi.backward_plan(n, f, bmax, d)
+    assert pl["sorted"] == 1 and pl["windows"] > 1 and pl["features_per_group"] == 1
+    bw, nw = pl["bins_per_window"], pl["windows"]
+    assert bw <= 4096 and bw * nw >= bmax and bw * (nw - 1) < bmax
+    assert pl["lds_bytes"] <= 80 * 1024
+    assert pl["workspace_bytes"] >= pl["chunks"] * f * bmax * 2 * d * 4
+    lin = capi.backward_plan(n, f, bmax, d, linear0=True) if d <= 64 else None
+    assert lin is None or lin["sorted"] == 0
 
 
 def test_timing_api_without_a_device():

@@ -245,6 +245,42 @@ def test_global_cell_histogram_matches_lds_cells(cfg, n, tune, c_oracle):
     _check_backward(w, g, *glob, c_oracle)
 
 
+# (N, F, max bins, d): several sub-tiles and chunks a window; int16 and int32
+# bin indices; 10% of x exactly on an edge, so rows on a window's first edge
+# take the bin below from the row staged under the window
+BIN_WINDOWS = [(20000, 5, 1024, 32), (9000, 2, 40000, 4), (12000, 3, 700, 62), (6000, 4, 48, 256)]
+
+
+@pytest.mark.parametrize("shape", BIN_WINDOWS, ids=[f"{n}x{f}x{b}x{d}" for n, f, b, d in BIN_WINDOWS])
+def test_bin_windows_backward(shape, tune, c_oracle):
+    """Tables beyond LDS: the sorted path in windows of bins.  dx, dW, db at
+    the fp32 bar of the float64 oracle, bitwise equal on a repeat, and within
+    the same bar of the fallback kernels (another summation order)."""
+    from piecewiselinearembeddings_optimized_amd import capi
+
+    n, f, bmax, d = shape
+    w = wide_case(n, f, bmax, d, seed=7 + bmax)
+    pl = capi.backward_plan(n, f, bmax, d)
+    print(f"bin windows {w.name} plan windows={pl['windows']} bins_per_window={pl['bins_per_window']} "
+          f"chunks={pl['chunks']}", flush=True)
+    assert pl["sorted"] == 1 and pl["windows"] > 1
+    x, e, iw, nb, wt, _ = _inputs(w)
+    _, idx = ops.forward(x, e, iw, nb, wt, torch.float32)
+    g = np.random.default_rng(bmax).standard_normal((n, f, d)).astype(np.float32)
+    got = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, True, True, True)
+    again = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, True, True, True)
+    torch.cuda.synchronize()
+    for a, b in zip(got, again):
+        assert torch.equal(a, b)
+    _check_backward(w, g, *got, c_oracle)
+    dx_only, _, _ = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, True, False, False)
+    assert torch.equal(dx_only, got[0])
+    tune("BWD_SIMPLE", 1)
+    fb = ops.backward_with_bias(_t(g), x, e, iw, nb, wt, idx, torch.float32, True, True, True)
+    torch.cuda.synchronize()
+    _check_backward(w, g, *fb, c_oracle)
+
+
 def test_wide_tables_through_the_c_abi(c_oracle):
     """ple_forward_launch / ple_backward_launch take the wide shapes directly
     (no PLE_E_UNSUPPORTED), with int32 indices."""
