@@ -59,8 +59,10 @@ struct FwdArgs {
     int out_nt;   // table kernel: output stores with the non-temporal hint (see forward_run)
     // wide-table kernel: checkpoint stride (bins), LDS offsets (floats) of
     // the weight stage and of the edge / inverse-width tables, and whether
-    // the edges and inverse widths are staged in LDS (else read from global)
-    int S, stage_off, edge_off, edges_lds;
+    // the edges and inverse widths are staged in LDS (else every ES-th edge
+    // is, for the first steps of the bin search, and the rest is read from
+    // global memory)
+    int S, stage_off, edge_off, edges_lds, ES;
 };
 
 size_t fwd_lds_bytes(int64_t FS, int64_t B, int64_t D) {
@@ -385,6 +387,37 @@ constexpr int kWideStage = 4096;         // weights staged per step of the prefi
 // inverse widths are in LDS when they fit (edges_lds), else the bin search
 // reads them from global memory.  Stores, epilogues and ReLU bits as in the
 // table kernel (one feature a group).
+// find_bin over edges in global memory, with every es-th edge (es a power
+// of two) in LDS: the sampled edges narrow the search to es - 1 edges, read
+// from global memory.  For sorted edges the same bin as find_bin (the count
+// of edges <= v, each level an upper bound); NaN walks to the top again.
+__device__ __forceinline__ int find_bin_sampled(float v, const float *cs, int es_log, const float *e, int n) {
+    const int nc = (n >> es_log) + 1;         // sampled edges 0, es, 2 es, ... <= n
+    int lo = 0, hi = nc;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (v < cs[mid]) hi = mid;
+        else lo = mid + 1;
+    }
+    // lo sampled edges are <= v: the count lies in [(lo - 1) es + 1, lo es]
+    int k;
+    if (lo == 0) {
+        k = 0;
+    } else {
+        int a0 = ((lo - 1) << es_log) + 1;
+        int b1 = min((lo << es_log) - 1, n) + 1;
+        while (a0 < b1) {
+            const int mid = (a0 + b1) >> 1;
+            if (v < e[mid]) b1 = mid;
+            else a0 = mid + 1;
+        }
+        k = a0 - 1;
+    }
+    k = k < 0 ? 0 : k;
+    k = k > n - 1 ? n - 1 : k;
+    return k;
+}
+
 template <int Q, int OUT, int EPI, int VEC, typename IdxT>
 __global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
     constexpr int kWaves = kWideFB / kWave;
@@ -394,7 +427,7 @@ __global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
     const int B = a.B, D = a.D, F = a.F, S = a.S;
     float *cp = smem;                            // [ceil(B / S)][DC]
     float *stage = smem + a.stage_off;           // [kWideStage]
-    float *sedge = smem + a.edge_off;            // [B + 1] (edges_lds)
+    float *sedge = smem + a.edge_off;            // [B + 1] (edges_lds), else [B / ES + 1] sampled edges
     float *siw = sedge + (B + 1);                // [B]     (edges_lds)
 
     int f, c;
@@ -412,36 +445,71 @@ __global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
     const float *wf = a.weight + static_cast<int64_t>(f) * B * D;
     const float *ef = a.edges + static_cast<int64_t>(f) * (B + 1);
     const float *iwf = a.iw + static_cast<int64_t>(f) * B;
+    const int es_log = __ffs(a.ES) - 1;
+    // dst[i] = get(i) for i < count, eight loads in flight per thread (a
+    // plain loop waits for each load before the next)
+    auto stage_lds = [&](float *dst, int count, auto get) __attribute__((always_inline)) {
+        for (int i0 = tid; i0 < count; i0 += 8 * kWideFB) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = get(min(i0 + u * kWideFB, count - 1));
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (i0 + u * kWideFB < count) dst[i0 + u * kWideFB] = v[u];
+        }
+    };
     if (a.edges_lds) {
         // the search reads edges 0..n, the fraction inverse widths 0..n-1
-        for (int i = tid; i <= n; i += kWideFB) sedge[i] = ef[i];
-        for (int i = tid; i < n; i += kWideFB) siw[i] = iwf[i];
+        stage_lds(sedge, n + 1, [&](int i) { return ef[i]; });
+        stage_lds(siw, n, [&](int i) { return iwf[i]; });
+    } else {
+        stage_lds(sedge, (n >> es_log) + 1, [&](int i) { return ef[i << es_log]; });
     }
 
     // ---- prefix checkpoints ------------------------------------------------
     // Weight rows 0..n-2 enter prefixes (the prefix of bin k sums bins < k,
     // all identity-mapped below the last bin).  Blocks of kb bins are staged
-    // (contiguous rows of W), then the threads of columns 0..D-1 fold them.
+    // (contiguous rows of W); one lane per column turns the block in place
+    // into its running prefix -- one chain of additions in bin order, the
+    // LDS reads of eight steps ahead of them -- and then all threads copy
+    // the block's checkpoints (bins that are multiples of S).
     const int kb = kWideStage / Dw;
     float acc = 0.0f;
-    int next_cp = 0, m_cp = 0;
     for (int k0 = 0; k0 < n; k0 += kb) {
         const int nk = min(kb, n - k0);
         const int nterm = min(nk, n - 1 - k0);       // rows of this block that enter a prefix
-        for (int i = tid; i < nk * Dw; i += kWideFB) {
+        stage_lds(stage, nk * Dw, [&](int i) {
             const int t = i / Dw;
-            stage[i] = t < nterm ? quant<Q>(wf[static_cast<int64_t>(k0 + t) * D + c0 + (i - t * Dw)]) : 0.0f;
-        }
+            // (rows past the prefixes read row k0 and add zero)
+            const float w = quant<Q>(wf[static_cast<int64_t>(k0 + (t < nterm ? t : 0)) * D + c0 + (i - t * Dw)]);
+            return t < nterm ? w : 0.0f;
+        });
         __syncthreads();
         if (tid < Dw) {
-            for (int t = 0; t < nk; ++t) {
-                if (k0 + t == next_cp) {
-                    cp[m_cp * Dw + tid] = acc;
-                    ++m_cp;
-                    next_cp += S;
+            int t0 = 0;
+            for (; t0 + 16 <= nk; t0 += 16) {
+                float v16[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) v16[u] = stage[(t0 + u) * Dw + tid];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    stage[(t0 + u) * Dw + tid] = acc;
+                    acc += v16[u];
                 }
-                acc += stage[t * Dw + tid];
             }
+            for (; t0 < nk; ++t0) {
+                const float v = stage[t0 * Dw + tid];
+                stage[t0 * Dw + tid] = acc;
+                acc += v;
+            }
+        }
+        __syncthreads();
+        const int m_first = (k0 + S - 1) / S;
+        const int m_end = (k0 + nk + S - 1) / S;   // checkpoints m S in [k0, k0 + nk)
+        for (int i = tid; i < (m_end - m_first) * Dw; i += kWideFB) {
+            const int mm = i / Dw;
+            const int j = i - mm * Dw;
+            cp[(m_first + mm) * Dw + j] = stage[((m_first + mm) * S - k0) * Dw + j];
         }
         __syncthreads();
     }
@@ -481,7 +549,7 @@ __global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
         const int64_t pn = n0 + lane;
         const bool pvalid = pn < n_end;
         const float v = pvalid ? a.x[pn * F + f] : 0.0f;
-        const int k = find_bin(v, e_row, n);
+        const int k = a.edges_lds ? find_bin(v, e_row, n) : find_bin_sampled(v, sedge, es_log, ef, n);
         const float qf = quant<Q>((v - e_row[k]) * iw_row[k]);
         if (pvalid && cc == 0) static_cast<IdxT *>(a.idx)[pn * F + f] = static_cast<IdxT>(k);
 
@@ -498,10 +566,23 @@ __global__ __launch_bounds__(kWideFB) void ple_fwd_wide_kernel(FwdArgs a) {
                 const int m = ks / S;
                 float P[VEC], W[VEC];
                 lds_load_vec<VEC>(cp + m * Dw + o_u * VEC, P);
-                for (int i = m * S; i < ks; ++i) {
-                    const float *wi = wcol + static_cast<int64_t>(i) * D;
+                // the rows between the checkpoint and the bin, eight loads
+                // ahead of their additions (in bin order)
+                for (int i0 = m * S; i0 < ks; i0 += 8) {
+                    float w8[8][VEC];
 #pragma unroll
-                    for (int h = 0; h < VEC; ++h) P[h] += quant<Q>(wi[h]);
+                    for (int u = 0; u < 8; ++u) {
+                        const float *wi = wcol + static_cast<int64_t>(min(i0 + u, ks - 1)) * D;
+#pragma unroll
+                        for (int h = 0; h < VEC; ++h) w8[u][h] = wi[h];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        if (i0 + u < ks) {
+#pragma unroll
+                            for (int h = 0; h < VEC; ++h) P[h] += quant<Q>(w8[u][h]);
+                        }
+                    }
                 }
                 const float *wk = wcol + static_cast<int64_t>(phys_bin(ks, n, B)) * D;
 #pragma unroll
@@ -533,7 +614,7 @@ struct FwdPlan {
     int64_t NC;
     size_t lds;
     bool wide = false;                  // ple_fwd_wide_kernel
-    int S = 1, stage_off = 0, edge_off = 0, edges_lds = 0;
+    int S = 1, stage_off = 0, edge_off = 0, edges_lds = 0, ES = 1;
 };
 
 // Wide tables: the prefix checkpoints take at most kWideCpBudget bytes of
@@ -541,6 +622,7 @@ struct FwdPlan {
 // them when they fit kWideEdgeBudget.
 constexpr size_t kWideCpBudget = 96 * 1024;
 constexpr size_t kWideEdgeBudget = 40 * 1024;
+constexpr size_t kWideSampleBudget = 16 * 1024;
 
 // Rows of more than a wave's lanes (D / vec > 64) are cut into NCC chunks of
 // DC columns (a multiple of vec), as even as the lanes allow.
@@ -564,15 +646,24 @@ void plan_wide(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, FwdPla
     pl.stage_off = static_cast<int>(align_up(static_cast<size_t>(ncp * Dc), 4));
     pl.edge_off = pl.stage_off + kWideStage;
     pl.edges_lds = static_cast<size_t>(2 * B + 1) * 4 <= kWideEdgeBudget ? 1 : 0;
-    pl.lds = 4 * (static_cast<size_t>(pl.edge_off) + (pl.edges_lds ? static_cast<size_t>(2 * B + 1) : 0));
+    // otherwise every ES-th edge, ES the smallest power of two (at least 8)
+    // whose samples fit kWideSampleBudget
+    pl.ES = 1;
+    if (!pl.edges_lds) {
+        pl.ES = 8;
+        while (static_cast<size_t>(B / pl.ES + 1) * 4 > kWideSampleBudget) pl.ES *= 2;
+    }
+    const size_t edge_floats = pl.edges_lds ? static_cast<size_t>(2 * B + 1) : static_cast<size_t>(B / pl.ES + 1);
+    pl.lds = 4 * (static_cast<size_t>(pl.edge_off) + edge_floats);
     pl.G = static_cast<int>(F) * pl.NCC;
-    // chunks: about two workgroups per CU over the grid, each writing at least
-    // kOutPerTable times the weight bytes its prefix pass reads
-    const int64_t target = 2 * static_cast<int64_t>(device_cu_count());
+    // chunks: one round of the workgroups the CUs hold at once (LDS), so
+    // every workgroup folds its prefix at the same time; the weights a fold
+    // reads again per chunk come from the caches
+    // (PLE_TUNE_FWD_WG_PER_CU: that many per CU)
+    const int wg_env = tuning(PLE_TUNE_FWD_WG_PER_CU);
+    const int64_t resident = std::max<int64_t>(1, static_cast<int64_t>(kLdsMax / pl.lds));
+    const int64_t target = (wg_env > 0 ? wg_env : resident) * device_cu_count();
     int64_t c = (target + pl.G - 1) / pl.G;
-    const int64_t min_nc = (static_cast<int64_t>(kOutPerTable) * B * 4 + out_bytes - 1) / out_bytes;
-    const int64_t c_tbl = (N + min_nc - 1) / min_nc;
-    if (c > c_tbl) c = c_tbl;
     const int64_t max_c = (N + kWave - 1) / kWave;
     if (c > max_c) c = max_c;
     if (c < 1) c = 1;
@@ -591,8 +682,10 @@ void plan_wide(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, FwdPla
 // us, c3 186 -> 155 us, c4 517 -> 221 us, c1 unchanged (its plan is the same).
 // PLE_TUNE_FWD_FS / PLE_TUNE_FWD_WG_PER_CU override the two choices.
 
-// out16: the output's base address is 16-byte aligned (8 outputs per lane)
-bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, bool aligned16, bool out16, FwdPlan &pl) {
+// out16: the output's base address is 16-byte aligned (8 outputs per lane);
+// relu: the epilogue writes ReLU pass bits
+bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, bool aligned16, bool out16, bool relu,
+                  FwdPlan &pl) {
     // 16-bit outputs: 8 per lane (one 16-byte store) when D allows, so a
     // store instruction carries as many bytes as fp32's 4 per lane
     // Even D not a multiple of 4: 2 per lane (8-byte stores), half the store
@@ -600,6 +693,25 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
     pl.vec = (D % 4 == 0 && aligned16) ? 4 : ((D % 2 == 0 && aligned16 && tuning(PLE_TUNE_FWD_VEC) != 1) ? 2 : 1);
     if (out_bytes == 2 && D % 8 == 0 && aligned16 && out16 && tuning(PLE_TUNE_FWD_VEC) != 4) pl.vec = 8;
     plan_chunks(D, pl);
+    // Tables beyond LDS: rows cut into narrower column chunks (one feature a
+    // group) until a chunk's tables fit, while a chunk's segment of a row
+    // keeps 64 bytes, before the wide-table kernel.  At N = 65536, fp32:
+    // B = 1024, d = 32 (two chunks of 16) 601 -> 328 us, B = 700, d = 64
+    // (three of 24 or 16) 567 -> 504 us; B = 2048, d = 16 (two of 8, 32-byte
+    // segments) 137 -> 159 us, so not there.  (Not with a ReLU: a row's pass
+    // bits are gathered from the lanes of one chunk.)
+    if (!relu && tuning(PLE_TUNE_FWD_WIDE) != 1) {
+        const int64_t U = D / pl.vec;
+        int64_t ncc = pl.NCC;
+        FwdPlan t = pl;
+        while (fwd_lds_bytes(1, B, t.DC) > kLdsMax && t.DC > t.vec) {
+            ++ncc;
+            const int64_t dcu = (U + ncc - 1) / ncc;
+            t.DC = static_cast<int>(dcu * t.vec);
+            t.NCC = static_cast<int>((U + dcu - 1) / dcu);
+        }
+        if (t.DC * out_bytes >= 64 || t.NCC == pl.NCC) pl = t;
+    }
     if (fwd_lds_bytes(1, B, pl.DC) > kLdsMax || tuning(PLE_TUNE_FWD_WIDE) == 1) {
         plan_wide(N, F, B, D, out_bytes, pl);
         return true;
@@ -770,7 +882,8 @@ int forward_run(const ForwardRequest &r) {
     const bool aligned16 = (reinterpret_cast<uintptr_t>(r.out) % (4 * out_bytes) == 0) &&
                            (reinterpret_cast<uintptr_t>(r.weight) % 16 == 0);
     FwdPlan pl;
-    if (!plan_forward(r.N, r.F, r.B, r.D, out_bytes, aligned16, reinterpret_cast<uintptr_t>(r.out) % 16 == 0, pl))
+    if (!plan_forward(r.N, r.F, r.B, r.D, out_bytes, aligned16, reinterpret_cast<uintptr_t>(r.out) % 16 == 0,
+                      r.relu != 0, pl))
         return PLE_E_UNSUPPORTED;
     FwdArgs a;
     a.x = r.x; a.edges = r.edges; a.iw = r.iw; a.nbins = r.nbins; a.weight = r.weight;
@@ -792,7 +905,7 @@ int forward_run(const ForwardRequest &r) {
         const int64_t row = r.F * r.D * out_bytes;
         a.out_nt = seg % 64 == 0 && row % 64 == 0 && reinterpret_cast<uintptr_t>(r.out) % 64 == 0;
     }
-    a.S = pl.S; a.stage_off = pl.stage_off; a.edge_off = pl.edge_off; a.edges_lds = pl.edges_lds;
+    a.S = pl.S; a.stage_off = pl.stage_off; a.edge_off = pl.edge_off; a.edges_lds = pl.edges_lds; a.ES = pl.ES;
     const int64_t grid = kNumXcd * tiles_per_xcd(pl.G, pl.C);
     if (grid > INT32_MAX) return PLE_E_TOO_LARGE;
     const int idxb = idx_bytes_for(r.B);
