@@ -150,7 +150,8 @@ def _module_bench(args):
                                                                 version=args.version).to(dev)
     torch.nn.init.uniform_(m.linear.weight, -0.2, 0.2)
     ops = torch.ops.rtdl_num_embeddings_cuda
-    x = torch.from_numpy(w.x).to(dev).requires_grad_(True)
+    x_plain = torch.from_numpy(w.x).to(dev)
+    x_grad = x_plain.clone().requires_grad_(True)
     g = torch.randn((n, f, d), device=dev, generator=torch.Generator(dev).manual_seed(0))
 
     def unfused(xx):
@@ -162,28 +163,39 @@ def _module_bench(args):
             x_ple = m.activation(x_ple)
         return x_ple if m.linear0 is None else m.linear0(xx) + x_ple
 
-    def timed(fn, backward):
+    # The reference harness's step (tests/test_ple_cuda_benchmark.py:646-657): gradients set to None, then
+    # forward and backward; its x needs no gradient (:1372-1379).  `*_fwdbwd_dx_ms`: the same with x
+    # requiring a gradient too (dx, and x.grad set to None each step).
+    def timed(fn, backward, x):
         def step():
+            if backward:
+                m.zero_grad(set_to_none=True)
+                x.grad = None
             out = fn(x)
             if backward:
                 out.backward(g)
         for _ in range(max(args.warmup, 1)):
             step()
         torch.cuda.synchronize()
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        t0.record()
-        for _ in range(args.steps):
-            step()
-        t1.record()
-        torch.cuda.synchronize()
-        return t0.elapsed_time(t1) / args.steps
+        # median of five regions of K steps (the GPU's clocks move between regions)
+        t = []
+        for _ in range(5):
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(args.steps):
+                step()
+            t1.record()
+            torch.cuda.synchronize()
+            t.append(t0.elapsed_time(t1) / args.steps)
+        return sorted(t)[2]
 
     res = {}
     for name, fn in (("fused", m), ("reference_ops", unfused)):
         with torch.no_grad():
-            res[f"{name}_fwd_ms"] = timed(fn, False)
-        res[f"{name}_fwdbwd_ms"] = timed(fn, True)
+            res[f"{name}_fwd_ms"] = timed(fn, False, x_plain)
+        res[f"{name}_fwdbwd_ms"] = timed(fn, True, x_plain)
+        res[f"{name}_fwdbwd_dx_ms"] = timed(fn, True, x_grad)
     line = {
         "metric": f"module fwd+bwd samples/s (version {args.version}, activation={args.activation}, {w.name})",
         "value": n / (res["fused_fwdbwd_ms"] * 1e-3),
