@@ -14,7 +14,8 @@ reference kernel for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters to
 bytes).  ``--mode module`` times the whole module in the reference
 benchmark's configuration (version B, no activation; forward and
 forward+backward), fused against the reference's op sequence (the forward
-operator followed by PyTorch's linear0 and residual add).  ``--mode encode``
+operator followed by PyTorch's linear0 and residual add); ``--compile`` adds
+both under torch.compile as the reference harness compiles them.  ``--mode encode``
 times the dense encoding kernels (``encode`` / ``encode_backward``).
 
 Timing: W untimed warm-up steps; the forward and backward operators timed
@@ -52,6 +53,8 @@ def _parse():
     ap.add_argument("--mode", choices=("fwdbwd", "fwd", "module", "encode", "copy"), default="fwdbwd")
     ap.add_argument("--version", choices=("A", "B"), default="B", help="module version (--mode module)")
     ap.add_argument("--activation", action="store_true", help="ReLU in the module (--mode module)")
+    ap.add_argument("--compile", action="store_true",
+                    help="also time torch.compile(inductor, default mode, dynamic, fullgraph) (--mode module)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=None,
                     help="rows of the workload timed on the CPU (default: the whole batch, up to a 1.6 GB "
@@ -196,6 +199,29 @@ def _module_bench(args):
             res[f"{name}_fwd_ms"] = timed(fn, False, x_plain)
         res[f"{name}_fwdbwd_ms"] = timed(fn, True, x_plain)
         res[f"{name}_fwdbwd_dx_ms"] = timed(fn, True, x_grad)
+    if args.compile:
+        # The reference harness's compiled execution (tests/test_ple_cuda_benchmark.py:128-137,
+        # 740-746): inductor, default mode, dynamic and fullgraph; compiled and stabilised before
+        # timing at the benchmark shape, at half the batch (the dynamic shape) and three more calls
+        # (:748-774).
+        half = n // 2
+
+        def stabilise(fn, backward):
+            for xx, gg in ((x_plain, g), (x_plain[:half], g[:half]), (x_plain, g), (x_plain, g), (x_plain, g)):
+                if backward:
+                    m.zero_grad(set_to_none=True)
+                    fn(xx).backward(gg)
+                else:
+                    fn(xx)
+            torch.cuda.synchronize()
+
+        for name, fn in (("fused", m), ("reference_ops", unfused)):
+            cfn = torch.compile(fn, backend="inductor", mode="default", dynamic=True, fullgraph=True)
+            with torch.no_grad():
+                stabilise(cfn, False)
+                res[f"compiled_{name}_fwd_ms"] = timed(cfn, False, x_plain)
+            stabilise(cfn, True)
+            res[f"compiled_{name}_fwdbwd_ms"] = timed(cfn, True, x_plain)
     line = {
         "metric": f"module fwd+bwd samples/s (version {args.version}, activation={args.activation}, {w.name})",
         "value": n / (res["fused_fwdbwd_ms"] * 1e-3),
