@@ -313,6 +313,38 @@ def test_wide_tables_through_the_c_abi(c_oracle):
     _check_backward(w, g.cpu().numpy(), gx, gw, None, c_oracle)
 
 
+@pytest.mark.parametrize("bmax", [8192, 40000])
+def test_sampled_edge_search_special_values(bmax, c_oracle):
+    """Edges beyond LDS: the wide kernel keeps every ES-th edge in LDS and
+    finishes the bin search in global memory.  Every edge exactly (the sampled
+    ones included), its float neighbours, midpoints, far outside both ends,
+    +-inf and NaN: bin indices against searchsorted, outputs bit-exact against
+    the C mirror, for the full feature and a ragged one (fewer real bins)."""
+    rng = np.random.default_rng(bmax)
+    f, d = 2, 4
+    bins = [np.cumsum(rng.uniform(0.01, 1.0, bmax + 1)).astype(np.float32) - bmax * 0.25,
+            np.cumsum(rng.uniform(0.01, 1.0, bmax // 3 + 1)).astype(np.float32)]
+    edges, iw, nbins = workloads.pad_bins(bins)
+    cols = []
+    for e in bins:
+        mids = ((e[:-1].astype(np.float64) + e[1:]) / 2).astype(np.float32)
+        up = np.nextafter(e, np.float32(np.inf))
+        dn = np.nextafter(e, np.float32(-np.inf))
+        special = np.array([np.nan, np.inf, -np.inf, e[0] - 1e6, e[-1] + 1e6], np.float32)
+        cols.append(np.concatenate([e, up, dn, mids, special]))
+    n = max(c.size for c in cols)
+    x = np.stack([np.resize(c, n) for c in cols], axis=1).astype(np.float32)
+    wt = rng.uniform(-0.5, 0.5, (f, bmax, d)).astype(np.float32)
+    w = workloads.Workload(f"sampled{bmax}", x, bins, edges, iw, nbins, wt, np.zeros((f, d), np.float32))
+    print(f"sampled edge search {w.name} n={n}", flush=True)
+    X, E, IW, NB, WT, _ = _inputs(w)
+    out, idx = ops.forward(X, E, IW, NB, WT, torch.float32)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(idx.cpu().numpy().astype(np.int64), po.bin_indices(x, edges, nbins))
+    mirror, _ = c_oracle.forward_f32(x, edges, iw, nbins, wt)
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), mirror.view(np.uint32))
+
+
 def test_module_on_wide_bins(c_oracle):
     """The module end to end on 450- to 600-bin features at d = 48: forward
     against its own CPU path (the dense upstream formulation) at the
