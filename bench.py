@@ -417,16 +417,19 @@ def main():
 
     fwd_bytes, bwd_bytes = workloads.algorithmic_bytes(n, f, bmax, d, out_bytes=out_bytes)
     # The backward's plan decides what its timed kernel writes: with one chunk
-    # the sorted path's gradient kernel writes dW / db itself, otherwise a
-    # finalize kernel does (from chunk partials).  The fallback path's timer
-    # spans its dx and histogram kernels.
+    # (and one bin window) the sorted path's and the matrix-core path's
+    # gradient kernel writes dW / db itself, otherwise a finalize kernel does
+    # (from chunk partials).  The fallback path's timer spans its dx and
+    # histogram kernels.
     plan = capi.backward_plan(n, f, bmax, d, grad_dtype=g.dtype, quant_dtype=quant, grad_output=g)
     bwd_kernel_bytes = bwd_bytes
-    if not (plan["sorted"] and plan["chunks"] == 1):
+    single = (plan["sorted"] or plan["matrix_cores"]) and plan["chunks"] == 1 and plan["windows"] == 1
+    if not single:
         bwd_kernel_bytes -= f * bmax * d * 4 + f * d * 4
     kernels = {}
     fwd_name = "ple_fwd_kernel"
-    bwd_name = "ple_bwd_fused_kernel" if plan["sorted"] else "ple_bwd_simple_dx_kernel+ple_bwd_simple_hist_kernel"
+    bwd_name = ("ple_bwd_mfma_kernel" if plan["matrix_cores"] else
+                "ple_bwd_fused_kernel" if plan["sorted"] else "ple_bwd_simple_dx_kernel+ple_bwd_simple_hist_kernel")
     for name, key, nbytes in ((fwd_name, "fwd", fwd_bytes), (bwd_name, "bwd", bwd_kernel_bytes)):
         total_ms, launches = kern[key]
         if launches == 0:

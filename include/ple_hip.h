@@ -162,7 +162,8 @@ int ple_backward_launch_noalloc(const void *grad_output, const float *x, const f
  *   chunks             sample chunks with dW / db partials in the workspace
  *                      (sorted path with 1 chunk: the gradient kernel writes
  *                      grad_weight / grad_bias itself, no finalize kernel)
- *   features_per_group features per gradient-kernel workgroup (sorted path)
+ *   features_per_group features per gradient-kernel workgroup (sorted and
+ *                      matrix-core paths)
  *   columns_per_lane   gradient elements a lane holds per row (sorted path)
  *   lanes_per_row      lanes that share a row (sorted path)
  *   threads            gradient-kernel workgroup size
@@ -173,6 +174,10 @@ int ple_backward_launch_noalloc(const void *grad_output, const float *x, const f
  *                      in LDS (sorted path; B when all of them fit)
  *   windows            workgroups per feature group, one per window of bins
  *                      (sorted path; 1 when all bins fit)
+ *   matrix_cores       1: the histograms as one-hot products on the matrix
+ *                      cores (16-bit gradients in their own dtype, rows of 8,
+ *                      16, 24 or 32 columns, at most 96 bins, at most 8
+ *                      chunks); sorted is 0 then
  */
 typedef struct ple_backward_plan_info {
     int sorted;
@@ -185,6 +190,7 @@ typedef struct ple_backward_plan_info {
     size_t workspace_bytes;
     int bins_per_window;
     int windows;
+    int matrix_cores;
 } ple_backward_plan_info_t;
 int ple_backward_plan_query(const void *grad_output, int64_t N, int64_t F, int64_t B, int64_t D,
                             int grad_dtype, int quant_dtype, int relu, int linear0,
@@ -275,9 +281,13 @@ int ple_encode_backward_launch(const float *grad_output, const float *x, const f
  *   PLE_TUNE_BWD_SIMPLE_GLOBAL 1: their histogram cells in global memory
  *   PLE_TUNE_BWD_VEC        1: one gradient element per lane; 4: at most four
  *                           (no 8-element lanes for 16-bit gradients)
- *   PLE_TUNE_BWD_FS         features per backward sub-tile (1, 2, 4, 8, 16)
+ *   PLE_TUNE_BWD_FS         features per backward sub-tile (1, 2, 4, 8, 16;
+ *                           the matrix-core backward's groups: 1, 2, 4)
  *   PLE_TUNE_BWD_RB         reducer threads per backward workgroup (256 or 512)
  *   PLE_TUNE_BWD_WG_PER_CU  backward workgroups per CU
+ *   PLE_TUNE_BWD_MFMA       1: no matrix-core backward (the sorted path for
+ *                           16-bit gradients too); 2: the matrix-core backward
+ *                           for every shape it can take (also past 8 chunks)
  * A forced value the shape cannot take is ignored.  Returns the knob's
  * previous value, or PLE_E_BAD_SHAPE for an unknown knob.  Not synchronised
  * with launches running on other threads.
@@ -294,7 +304,8 @@ enum {
     PLE_TUNE_BWD_FS = 8,
     PLE_TUNE_BWD_RB = 9,
     PLE_TUNE_BWD_WG_PER_CU = 10,
-    PLE_TUNE_COUNT = 11,
+    PLE_TUNE_BWD_MFMA = 11,
+    PLE_TUNE_COUNT = 12,
 };
 int ple_set_tuning(int knob, int value);
 

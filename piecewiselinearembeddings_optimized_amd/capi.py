@@ -24,7 +24,7 @@ DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 # planner overrides (PLE_TUNE_* of the header; 0 = the planner's choice)
 TUNE = {
     "FWD_FS": 0, "FWD_WG_PER_CU": 1, "FWD_FB": 2, "FWD_VEC": 3, "FWD_WIDE": 4, "BWD_SIMPLE": 5,
-    "BWD_SIMPLE_GLOBAL": 6, "BWD_VEC": 7, "BWD_FS": 8, "BWD_RB": 9, "BWD_WG_PER_CU": 10,
+    "BWD_SIMPLE_GLOBAL": 6, "BWD_VEC": 7, "BWD_FS": 8, "BWD_RB": 9, "BWD_WG_PER_CU": 10, "BWD_MFMA": 11,
 }
 _DTYPE_CODES = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
 
@@ -57,6 +57,7 @@ class BackwardPlanInfo(ctypes.Structure):
         ("workspace_bytes", ctypes.c_size_t),
         ("bins_per_window", ctypes.c_int),
         ("windows", ctypes.c_int),
+        ("matrix_cores", ctypes.c_int),
     ]
 
 

@@ -1021,6 +1021,444 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// 16-bit gradients on the matrix cores
+// ---------------------------------------------------------------------------
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short v8s_t __attribute__((ext_vector_type(8)));
+
+// C += A B on a 32x32x16 matrix instruction, 16-bit operands, fp32
+// accumulation: A 32 x 16, lane l holding A[l % 32][8 (l / 32) + t] in its
+// element t (t = 0..7); B 16 x 32, lane l holding B[8 (l / 32) + t][l % 32];
+// C 32 x 32, lane l's register r holding C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]
+// (the layout checked on an MI355X against a host product, bf16 and fp16).
+// The eight 16-bit elements of an operand come packed in four dwords,
+// element t in bits 16 (t % 2) of dword t / 2.
+template <int GD>
+__device__ __forceinline__ f32x16_t mfma16(uint4 a, uint4 b, f32x16_t c) {
+    if constexpr (GD == PLE_DTYPE_BF16) {
+        typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0,
+                                                        0, 0);
+    } else {
+        typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0,
+                                                       0);
+    }
+}
+
+// Two 16-bit lanes at once.  min and negation are asm (the compiler turns the
+// equivalent vector code back into compares and selects); the multiply-add
+// that feeds the matrix instruction stays compiler code, so the compiler sees
+// the VALU write of that operand and keeps the wait states a matrix
+// instruction needs after it (an asm producer is invisible to that check)
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_min_u16(uint32_t a, uint32_t b) {
+    uint32_t r;
+    __asm__("v_pk_min_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ uint32_t pk_neg_u16(uint32_t a) {
+    uint32_t r;
+    __asm__("v_pk_sub_u16 %0, 0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+__device__ __forceinline__ uint32_t pk_mad_u16(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, b) +
+                                            __builtin_bit_cast(u16x2, c));
+}
+
+constexpr int kMB = 32;                            // samples per block (the products' K: two steps of 16)
+constexpr int kMfmaWaves = 8;                      // waves per workgroup
+constexpr int kMfmaBlock = kMfmaWaves * kWave;
+constexpr int kMfmaPF = 1;                         // steps whose loads are in flight (1 or 2)
+constexpr int kBPW = 2;                            // blocks of a wave in a step (worked on together)
+constexpr int kDxB = 16;                           // blocks whose dx a wave stores together
+// a staged row: 36 16-bit columns (72 bytes: the 8-byte reads of 32
+// consecutive rows meet distinct banks; columns D..35 stay zero, the
+// products' columns past D); a feature's rows of a step, then 32 bytes
+// that put the next feature's rows on other banks
+constexpr int kRowCols = 36;
+constexpr int kRowBytes = 2 * kRowCols;
+constexpr int kStepSamples = kMfmaWaves * kBPW * kMB;   // samples x features a step
+constexpr int kAreaPad = 48;   // the next feature's rows 12 banks on
+constexpr size_t kStageRows = static_cast<size_t>(kStepSamples) * kRowBytes + 4 * kAreaPad;
+// bytes of one stage: the rows, x [256 / FS][FS], the bin-index words (or
+// bytes)
+constexpr size_t kStageBytes = kStageRows + 4 * kStepSamples + 4 * kStepSamples;
+// per wave, not staged: the block's bins and q(frac) bits, 16-bit, [64]
+// each (lanes 32..63 write copies to the upper half), the dx of kDxB blocks
+constexpr int kMfmaWaveBytes = kBPW * (2 * 64 + 2 * 64) + 4 * kMB * kDxB;
+
+// A gradient already in the 16-bit quantisation dtype (bf16 or fp16) makes
+// every factor of the histograms exact in that dtype: bin k's bucket sum is
+// onehot_k^T g and its weighted sum (onehot_k * q(frac))^T g over the
+// samples, so the histograms of a block of 32 samples are two products of
+// the (bins x samples) one-hot matrices with the block's (samples x columns)
+// gradient, fp32-accumulated by the matrix instruction in an order it fixes:
+// deterministic, and no sort.
+//
+// One workgroup per (group of FS adjacent features, chunk of samples), in
+// steps of 256 / FS samples.  The workgroup loads a step together -- the FS
+// rows of a sample are contiguous, so the loads cover whole runs of memory
+// (rows of 48 bytes read one feature at a time, each at its sample's stride,
+// draw about half the rate) -- into LDS, two stages deep: the rows as
+// loaded, and each 32-sample block transposed for the products; x and the
+// bin indices likewise.  Wave w takes feature w % FS and block w / FS of each
+// step, and keeps that feature's histograms (NBT tiles of 32 bins, bucket
+// and weighted) in its accumulators.  Lane l holds sample l % 32 of the
+// block, the half l / 32 of its row (4 NQ columns): its bin, q(frac) and dx
+// come out of registers -- dx as the half-row's dot product with the
+// pre-scaled weight row of its bin (plus the lower bin's for x on a left
+// edge), the two halves added low half first.  At the end the waves of a
+// feature add their histograms in LDS in wave order, and they go, like the
+// sorted path's, to dW / db (one chunk) or to the chunk partials.  Rows of
+// D = 8 NQ columns (NQ = 1..4), at most 32 NBT bins; bin indices are uint8.
+template <int GD, int NBT, int NQ>
+__global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) {
+    constexpr int D = 8 * NQ;
+    constexpr int D2 = 2 * D;
+    constexpr int DH = 4 * NQ;   // columns of a half row
+    constexpr uint32_t kOne = GD == PLE_DTYPE_BF16 ? 0x3F80u : 0x3C00u;   // 1.0
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int B = a.B, F = a.F, FS = a.FS;
+    const int WPF = kMfmaWaves / FS;   // waves a feature
+    const int SPS = kMB * kBPW * WPF;  // samples a step
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    const int fl = wave % FS;   // the wave's feature in the group
+    const int wf = wave / FS;   // and its block in a step
+
+    int fg, c;
+    if (!decode_tile(blockIdx.x, a.G, a.C, fg, c)) return;
+    const int64_t n_begin = static_cast<int64_t>(c) * a.NC;
+    const int64_t n_end = min(a.N, n_begin + a.NC);
+    if (n_begin >= n_end) return;
+    const int f0 = fg * FS;
+    const int f = f0 + fl;
+    const bool fok = f < F;
+    const int n = fok ? clamp_nbins(a.nbins[f], B) : 1;
+    // the group's tables: [FS][B+1][D] q(W) * iw (row r: bin r - 1), [FS][B]
+    // iw, [FS][B+1] edges; then the two stages and the waves' areas, which
+    // the histograms [FS][B][2D] take over after the stream
+    float *s_qw = reinterpret_cast<float *>(lds + a.ro_qw) + fl * (B + 1) * D;
+    float *s_iw = reinterpret_cast<float *>(lds + a.ro_iw) + fl * B;
+    float *s_edge = reinterpret_cast<float *>(lds + a.ro_edge) + fl * (B + 1);
+    float *s_hist = reinterpret_cast<float *>(lds + a.ro_hist);
+    unsigned char *s_stage = lds + a.ro_desc;
+    unsigned char *wb = lds + a.ro_desc + 2 * kStageBytes + wave * kMfmaWaveBytes;
+    uint16_t *s_bin = reinterpret_cast<uint16_t *>(wb);                 // [kBPW][64] bin, 0xffff past the batch
+    uint16_t *s_q = reinterpret_cast<uint16_t *>(wb + kBPW * 128);      // [kBPW][64] q(frac) bits
+    float *s_dxb = reinterpret_cast<float *>(wb + kBPW * 256);          // [kDxB][32] dx
+    const int area = SPS * kRowBytes + kAreaPad;   // bytes of a feature's rows in a stage
+    auto st_rows = [&](int buf, int ff) { return s_stage + buf * kStageBytes + ff * area; };
+    auto st_x = [&](int buf) { return reinterpret_cast<float *>(s_stage + buf * kStageBytes + kStageRows); };
+    auto st_k = [&](int buf) {
+        return reinterpret_cast<uint32_t *>(s_stage + buf * kStageBytes + kStageRows + 4 * kStepSamples);
+    };
+
+    // ---- tables; the transposed blocks' columns past D stay zero ----------
+    for (int i = tid; i < FS * B; i += kMfmaBlock) {
+        const int ff = f0 + i / B;
+        reinterpret_cast<float *>(lds + a.ro_iw)[i] = ff < F ? a.iw[static_cast<int64_t>(ff) * B + i % B] : 0.0f;
+    }
+    for (int i = tid; i < FS * (B + 1); i += kMfmaBlock) {
+        const int ff = f0 + i / (B + 1);
+        reinterpret_cast<float *>(lds + a.ro_edge)[i] =
+            ff < F ? a.edges[static_cast<int64_t>(ff) * (B + 1) + i % (B + 1)] : 0.0f;
+    }
+    for (int i = tid; i < FS * (B + 1) * D; i += kMfmaBlock) {
+        const int ff = i / ((B + 1) * D);
+        const int rem = i - ff * (B + 1) * D;
+        const int rr = rem / D;
+        const int j = rem - rr * D;
+        const int kg = rr - 1;
+        const int fa = f0 + ff;
+        float w = 0.0f;
+        if (fa < F) {
+            const int na = clamp_nbins(a.nbins[fa], B);
+            const int64_t fb = static_cast<int64_t>(fa) * B;
+            if (kg >= 0 && kg < na) w = quant<GD>(a.weight[(fb + phys_bin(kg, na, B)) * D + j]) * a.iw[fb + kg];
+        }
+        reinterpret_cast<float *>(lds + a.ro_qw)[i] = w;
+    }
+    for (int i = tid; i < static_cast<int>(2 * kStageBytes / 4); i += kMfmaBlock)
+        reinterpret_cast<uint32_t *>(s_stage)[i] = 0u;
+    __syncthreads();
+
+    // ---- the loads of a step: kBPW NQ 8-byte pieces a lane in address order -
+    // piece u = tid + kMfmaBlock r of the step's SPS x FS D / 4 pieces:
+    // sample u / CPS, feature (u % CPS) / (D / 4), columns 4 (u % (D / 4)) ..
+    const int CPS = FS * D / 4;   // pieces a sample
+    const uint32_t rowFb = static_cast<uint32_t>(F) * D * 2;
+    const int gspan = min(FS, F - f0) * D * 2;   // bytes of the group's row that exist
+    constexpr int NP = kBPW * NQ;   // pieces a lane
+    uint32_t poff[NP];              // the piece's byte offset in the step's rows
+    int prow[NP];                   // its place in a stage
+    bool pok[NP];                   // its feature exists
+#pragma unroll
+    for (int r = 0; r < NP; ++r) {
+        const int u = tid + kMfmaBlock * r;
+        const int s = u / CPS, q = u - s * CPS;
+        const int ff = q / (D / 4), cq = q - ff * (D / 4);
+        poff[r] = static_cast<uint32_t>(s) * rowFb + static_cast<uint32_t>(q) * 8;
+        prow[r] = ff * area + s * kRowBytes + cq * 8;
+        pok[r] = f0 + ff < F;
+    }
+    // x and the bin indices: lane t < SPS FS takes x of (sample t / FS,
+    // feature t % FS) and the aligned 32-bit word holding its bin byte (a
+    // whole word, in the page of the byte: every load of the stream is then
+    // one instruction of one width, so the compiler's waits for a step's
+    // loads leave the later steps' loads in flight)
+    uint2 gq[kMfmaPF][NP];
+    float px[kMfmaPF];
+    uint32_t pk[kMfmaPF];
+    const int nsteps = static_cast<int>((n_end - n_begin + SPS - 1) / SPS);
+    auto load_step = [&](int p, int st) __attribute__((always_inline)) {
+        const int64_t s0 = n_begin + static_cast<int64_t>(st) * SPS;
+        const int ns = st < nsteps ? static_cast<int>(min(static_cast<int64_t>(SPS), n_end - s0)) : 0;
+        const __amdgpu_buffer_rsrc_t rs =
+            make_rsrc(static_cast<const char *>(a.g) + (s0 * F + f0) * static_cast<int64_t>(D) * 2,
+                      ns > 0 ? static_cast<uint32_t>(ns - 1) * rowFb + static_cast<uint32_t>(gspan) : 0u);
+#pragma unroll
+        for (int r = 0; r < NP; ++r) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, poff[r], 0, 0);
+            gq[p][r] = make_uint2(v[0], v[1]);
+        }
+        const int xs = tid / FS, xf = tid - xs * FS;
+        const bool xok = tid < SPS * FS && xs < ns && f0 + xf < F;
+        const int64_t pair = xok ? (s0 + xs) * F + f0 + xf : 0;
+        px[p] = a.x[pair];
+        const uint8_t *kb8 = static_cast<const uint8_t *>(a.idx) + pair;
+        pk[p] = *reinterpret_cast<const uint32_t *>(kb8 - (reinterpret_cast<uintptr_t>(kb8) & 3));
+    };
+    // a step's loads into LDS stage buf: the rows, feature by feature, x,
+    // the index words (or bytes)
+    auto stage_step = [&](int p, int buf) __attribute__((always_inline)) {
+        unsigned char *rows = st_rows(buf, 0);
+#pragma unroll
+        for (int r = 0; r < NP; ++r)
+            *reinterpret_cast<uint2 *>(rows + prow[r]) = pok[r] ? gq[p][r] : make_uint2(0u, 0u);
+        if (tid < SPS * FS) {
+            st_x(buf)[tid] = px[p];
+            st_k(buf)[tid] = pk[p];
+        }
+    };
+
+    // ---- the wave's block of each step --------------------------------------
+    const int sl = lane % 32;   // the lane's sample in a block
+    const int h = lane / 32;    // and its half row: columns DH h .. DH h + DH - 1
+    f32x16_t hb[NBT], hw[NBT];
+#pragma unroll
+    for (int T = 0; T < NBT; ++T)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) hb[T][r] = hw[T][r] = 0.0f;
+    // the one-hot operands, two samples a dword: per 16-bit half,
+    // m = min(bin ^ lane's bin, 1) is 0 on a hit, and m * (-v) + v gives v on
+    // a hit, 0 otherwise (v = 1.0 for the bucket sums, q(frac) for the
+    // weighted ones)
+    uint32_t lbin[NBT];
+#pragma unroll
+    for (int T = 0; T < NBT; ++T) lbin[T] = static_cast<uint32_t>(32 * T + sl) * 0x10001u;
+    const uint32_t one2 = kOne * 0x10001u;
+    const uint32_t negone2 = (0x10000u - kOne) * 0x10001u;
+    const uint32_t ones = 0x10001u;
+    // dx of the wave's last kDxB blocks, stored together and waited for at
+    // once: no store is left in flight among the loads (with one, the
+    // compiler's next wait for a load would cover every load in flight)
+    int nbuf = 0, buf_first = 0;
+    auto flush_dx = [&]() __attribute__((always_inline)) {
+        if (a.dx) {
+            for (int e = lane; e < nbuf * kBPW * kMB; e += kWave) {
+                const int bi = e / kMB;
+                const int64_t s = n_begin + static_cast<int64_t>(buf_first + bi / kBPW) * SPS +
+                                  (kBPW * wf + bi % kBPW) * kMB + (e - bi * kMB);
+                if (s < n_end) a.dx[s * F + f] = s_dxb[e];
+            }
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+        }
+    };
+    auto blocks = [&](int st, int buf) __attribute__((always_inline)) {
+        // the lane's sample of each block: bin, q(frac), left edge (x on e_k,
+        // k >= 1); the blocks' steps side by side
+        int k[kBPW];
+        bool valid[kBPW], edge[kBPW];
+        float qf[kBPW], dot[kBPW];
+        uint2 gv[kBPW][NQ];
+        const unsigned char *rows[kBPW];
+#pragma unroll
+        for (int i = 0; i < kBPW; ++i) {
+            const int sb0 = (kBPW * wf + i) * kMB;   // the block's first sample in the step
+            valid[i] = n_begin + static_cast<int64_t>(st) * SPS + sb0 + sl < n_end;
+            const int64_t pr = valid[i] ? (n_begin + static_cast<int64_t>(st) * SPS + sb0 + sl) * F + f : 0;
+            const int kshift = 8 * static_cast<int>((reinterpret_cast<uintptr_t>(a.idx) + pr) & 3);
+            const uint32_t kw = st_k(buf)[(sb0 + sl) * FS + fl];
+            k[i] = clamp_bin(static_cast<int>((kw >> kshift) & 0xffu), n);
+            const float xv = st_x(buf)[(sb0 + sl) * FS + fl];
+            const float e = s_edge[k[i]];
+            qf[i] = quant<GD>((xv - e) * s_iw[k[i]]);
+            edge[i] = k[i] > 0 && xv == e;
+            // the lane's half row
+            rows[i] = st_rows(buf, fl) + sb0 * kRowBytes;
+            const unsigned char *row = rows[i] + sl * kRowBytes + h * DH * 2;
+#pragma unroll
+            for (int j = 0; j < NQ; ++j) gv[i][j] = *reinterpret_cast<const uint2 *>(row + 8 * j);
+            // dx: the half row against bin k's pre-scaled weights
+            float w[DH];
+            lds_load_vec<DH>(s_qw + (k[i] + 1) * D + DH * h, w);
+            dot[i] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NQ; ++j) {
+                const uint32_t wd[2] = {gv[i][j].x, gv[i][j].y};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) dot[i] = fmaf(grad_elem<GD>(wd, t), w[4 * j + t], dot[i]);
+            }
+        }
+        // and bin k - 1's on a left edge, in a pass taken when the wave holds one
+        if (__ballot(edge[0] || edge[kBPW - 1])) {
+#pragma unroll
+            for (int i = 0; i < kBPW; ++i) {
+                float w[DH];
+                lds_load_vec<DH>(s_qw + k[i] * D + DH * h, w);
+                float d2 = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NQ; ++j) {
+                    const uint32_t wd[2] = {gv[i][j].x, gv[i][j].y};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) d2 = fmaf(grad_elem<GD>(wd, t), w[4 * j + t], d2);
+                }
+                if (edge[i]) dot[i] += d2;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kBPW; ++i) {
+            const float other = __shfl_xor(dot[i], 32);
+            // the same value from both halves
+            s_dxb[(nbuf * kBPW + i) * kMB + sl] = h == 0 ? dot[i] + other : other + dot[i];
+            s_bin[i * 64 + lane] = static_cast<uint16_t>(valid[i] ? k[i] : 0xffff);
+            s_q[i * 64 + lane] =
+                GD == PLE_DTYPE_BF16 ? static_cast<uint16_t>(__float_as_uint(qf[i]) >> 16) : f16_bits(qf[i]);
+        }
+        // the histograms: two steps of 16 samples a block; A = the one-hot
+        // (and q-weighted one-hot) rows of this lane's bins, B = the gradient:
+        // column sl of samples sb .. sb + 7 (zero past D)
+#pragma unroll
+        for (int i = 0; i < kBPW; ++i) {
+            const uint16_t *gcol = reinterpret_cast<const uint16_t *>(rows[i]) + sl;
+#pragma unroll
+            for (int ks = 0; ks < kMB / 16; ++ks) {
+                const int sb = 16 * ks + 8 * h;
+                v8s_t bv;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) bv[t] = static_cast<short>(gcol[(sb + t) * kRowCols]);
+                const uint4 bop = __builtin_bit_cast(uint4, bv);
+                const uint4 kb = *reinterpret_cast<const uint4 *>(s_bin + i * 64 + sb);
+                const uint4 qb = *reinterpret_cast<const uint4 *>(s_q + i * 64 + sb);
+                const uint32_t kv[4] = {kb.x, kb.y, kb.z, kb.w};
+                const uint32_t qv[4] = {qb.x, qb.y, qb.z, qb.w};
+                uint32_t nq[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) nq[j] = pk_neg_u16(qv[j]);
+#pragma unroll
+                for (int T = 0; T < NBT; ++T) {
+                    uint32_t ab[4], aw[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t m = pk_min_u16(kv[j] ^ lbin[T], ones);
+                        ab[j] = pk_mad_u16(m, negone2, one2);
+                        aw[j] = pk_mad_u16(m, nq[j], qv[j]);
+                    }
+                    hb[T] = mfma16<GD>(make_uint4(ab[0], ab[1], ab[2], ab[3]), bop, hb[T]);
+                    hw[T] = mfma16<GD>(make_uint4(aw[0], aw[1], aw[2], aw[3]), bop, hw[T]);
+                }
+            }
+        }
+        if (++nbuf == kDxB / kBPW) {
+            flush_dx();
+            nbuf = 0;
+            buf_first = st + 1;
+        }
+    };
+
+    // ---- steps: stage, refill, barrier, blocks ------------------------------
+    // (stage buf is rewritten two steps later, after the next step's barrier:
+    // every wave has left this step's blocks by then)
+    const bool mine = fok;
+#pragma unroll
+    for (int p = 0; p < kMfmaPF; ++p) load_step(p, p);
+    int st = 0;
+    for (; st + 1 < nsteps; st += 2) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            stage_step(p % kMfmaPF, p);
+            load_step(p % kMfmaPF, st + p + kMfmaPF);
+            __syncthreads();
+            if (mine && n_begin + static_cast<int64_t>(st + p) * SPS + kBPW * wf * kMB < n_end) blocks(st + p, p);
+        }
+    }
+    if (st < nsteps) {
+        stage_step(0, 0);
+        __syncthreads();
+        if (mine && n_begin + static_cast<int64_t>(st) * SPS + kBPW * wf * kMB < n_end) blocks(st, 0);
+    }
+    if (mine) flush_dx();
+    __syncthreads();
+
+    // ---- the feature's waves add their histograms in LDS, in wave order -----
+    float *hf = s_hist + fl * B * D2;
+    for (int w = 0; w < WPF; ++w) {
+        if (wf == w && fok && sl < D) {
+#pragma unroll
+            for (int T = 0; T < NBT; ++T)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int i = 32 * T + 8 * (r / 4) + 4 * h + r % 4;
+                    if (i < B) {
+                        float *hp = hf + i * D2;
+                        if (w == 0) {
+                            hp[sl] = hb[T][r];
+                            hp[D + sl] = hw[T][r];
+                        } else {
+                            hp[sl] += hb[T][r];
+                            hp[D + sl] += hw[T][r];
+                        }
+                    }
+                }
+        }
+        __syncthreads();
+    }
+
+    if (a.fin_fused) {
+        // one chunk: dW and db from the histograms (the finalize kernel's
+        // steps), one (feature, column) per group of kFinLanes lanes
+        constexpr int kGroups = kMfmaBlock / kFinLanes;
+        const int l = tid % kFinLanes;
+        for (int p0 = 0; p0 < FS * D; p0 += kGroups) {
+            const int pr = p0 + tid / kFinLanes;
+            const int ff = pr / D;
+            const int fa = f0 + ff;
+            const bool ok = pr < FS * D && fa < F;
+            const int j = ok ? pr - ff * D : 0;
+            const int nn = ok ? clamp_nbins(a.nbins[fa], B) : 0;
+            const float *hp = s_hist + (ok ? ff : 0) * B * D2 + j;
+            auto total = [&](int k, int hh) __attribute__((always_inline)) { return hp[k * D2 + hh * D]; };
+            float *dwc = ok && a.dw ? a.dw + static_cast<int64_t>(fa) * B * D + j : nullptr;
+            const float incl = dw_suffix(total, nn, B, D, l, dwc);
+            if (ok && l == 0 && a.db) a.db[static_cast<int64_t>(fa) * D + j] = incl;
+        }
+        return;
+    }
+    if (a.part) {
+        for (int ff = 0; ff < FS && f0 + ff < F; ++ff) {
+            const int nn = clamp_nbins(a.nbins[f0 + ff], B);
+            float *dst = a.part + (static_cast<int64_t>(c) * F + f0 + ff) * B * D2;
+            for (int i = tid; i < nn * D2; i += kMfmaBlock) dst[i] = s_hist[ff * B * D2 + i];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // fallback kernels
 // ---------------------------------------------------------------------------
 
@@ -1270,6 +1708,8 @@ constexpr size_t kReduceLdsTarget = 80 * 1024;
 
 struct BwdPlan {
     bool sorted;
+    int mfma_nbt = 0;   // > 0: ple_bwd_mfma_kernel with this many 32-bin tiles
+    int mfma_nq = 0;    // and rows of 8 mfma_nq columns
     bool hist_global;   // fallback: histogram cells in global memory (tables beyond LDS)
     int vec;
     int rb;          // reduce workgroup size
@@ -1321,6 +1761,20 @@ size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_
     return take.off;
 }
 
+// LDS of the matrix-core kernel: tables, the histogram, the waves' blocks
+// LDS of the matrix-core kernel: the FS features' tables, then the waves'
+// areas, which the histograms take over after the stream
+size_t mfma_layout(BwdArgs &g, int B, int D, int FS) {
+    LdsTaker take;
+    take(g.ro_qw, 4ull * FS * (B + 1) * D);
+    take(g.ro_iw, 4ull * FS * B);
+    take(g.ro_edge, 4ull * FS * (B + 1));
+    take(g.ro_desc, std::max<size_t>(2 * kStageBytes + static_cast<size_t>(kMfmaWaves) * kMfmaWaveBytes,
+                                     8ull * FS * B * D));
+    g.ro_hist = g.ro_desc;
+    return take.off;
+}
+
 // g_align16: the gradient's base address is 16-byte aligned; g16: the
 // gradient is a 16-bit type; raw_db: the bias gradient needs its own sums
 // (an fp32 gradient rounded to 16 bits, or linear0); lin: linear0 sums
@@ -1329,6 +1783,55 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
     pl.rb = kBlock;
     const int cus = device_cu_count();
     pl.sorted = false;
+    // A 16-bit gradient that is its own rounding (raw_db false for a 16-bit
+    // gradient: its quantisation dtype is its own), rows of 8, 16, 24 or 32
+    // columns, at most 96 bins (three tiles: the accumulators of four leave
+    // too few registers), a step's rows within 32-bit offsets: the
+    // matrix-core kernel, one workgroup per (group of FS features, chunk):
+    // FS = 4 adjacent features where LDS holds their tables (2, 1 else),
+    // chunks for a workgroup per CU (its eight waves fill the CU's two waves
+    // per SIMD) within the partials budget -- where that takes at most 8
+    // chunks: with more, shorter chunks' set-up, histogram merge and partials
+    // cost more than the sorted path (knob PLE_TUNE_BWD_MFMA: 1 never, 2
+    // whenever the shape allows).
+    const int mfma_knob = tuning(PLE_TUNE_BWD_MFMA);
+    if (g16 && !raw_db && !lin && g_align16 && D % 8 == 0 && D <= 32 && B <= 96 &&
+        static_cast<int64_t>(kStepSamples) * F * D * 2 < INT32_MAX && mfma_knob != 1 &&
+        tuning(PLE_TUNE_BWD_SIMPLE) == 0) {
+        BwdArgs geo{};
+        int fs = 4;
+        while (fs > 1 && (fs > F || mfma_layout(geo, static_cast<int>(B), static_cast<int>(D), fs) > kLdsMax))
+            fs /= 2;
+        if (tuning(PLE_TUNE_BWD_FS) == 1 || tuning(PLE_TUNE_BWD_FS) == 2 || tuning(PLE_TUNE_BWD_FS) == 4)
+            fs = std::min<int>(tuning(PLE_TUNE_BWD_FS), fs);
+        geo.FS = fs;
+        geo.G = static_cast<int>((F + fs - 1) / fs);
+        const int64_t per_chunk = F * B * 2 * D * 4;
+        int64_t c = (static_cast<int64_t>(cus) + geo.G - 1) / geo.G;
+        const int64_t budget_c = static_cast<int64_t>(kPartialBudget) / per_chunk;
+        if (c > budget_c) c = budget_c;
+        // a few steps for every chunk
+        const int64_t max_c = N / (static_cast<int64_t>(kMB) * 4 * (kMfmaWaves / fs));
+        if (c > max_c) c = max_c;
+        if (c < 1) c = 1;
+        if (c <= 8 || mfma_knob == 2) {
+            pl.mfma_nbt = static_cast<int>((B + 31) / 32);
+            pl.mfma_nq = static_cast<int>(D / 8);
+            pl.rb = kMfmaBlock;
+            pl.vec = 4;
+            int64_t nc = (N + c - 1) / c;
+            nc = (nc + kMB - 1) / kMB * kMB;
+            pl.NC = nc;
+            pl.lds = mfma_layout(geo, static_cast<int>(B), static_cast<int>(D), fs);
+            pl.C = pl.Cd = static_cast<int>((N + nc - 1) / nc);
+            pl.geo = geo;
+            if (pl.C > 1) {
+                pl.part_bytes = static_cast<size_t>(pl.Cd) * F * B * 2 * D * sizeof(float);
+                pl.part_db_bytes = static_cast<size_t>(pl.Cd) * F * D * sizeof(float);
+            }
+            return pl;
+        }
+    }
     // Sorted path: a sub-tile's gradient rows span less than 2^31 bytes
     // (32-bit buffer offsets); the bins of a workgroup fit the 12-bit field of
     // a piece -- all of them, or a window of them.
@@ -1533,6 +2036,16 @@ void launch_bwd(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, cons
     hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), s, t_slot.start, t_slot.stop, 0u, a);
 }
 
+template <int GD, int NBT>
+void launch_mfma(int nq, dim3 grid, size_t lds, hipStream_t s, const BwdArgs &a) {
+    switch (nq) {
+        case 1: launch_bwd((ple_bwd_mfma_kernel<GD, NBT, 1>), grid, dim3(kMfmaBlock), lds, s, a); break;
+        case 2: launch_bwd((ple_bwd_mfma_kernel<GD, NBT, 2>), grid, dim3(kMfmaBlock), lds, s, a); break;
+        case 3: launch_bwd((ple_bwd_mfma_kernel<GD, NBT, 3>), grid, dim3(kMfmaBlock), lds, s, a); break;
+        default: launch_bwd((ple_bwd_mfma_kernel<GD, NBT, 4>), grid, dim3(kMfmaBlock), lds, s, a); break;
+    }
+}
+
 // Lane-group width as a template argument (DPP reductions) for the 4- and
 // 2-float rows and the common one-column-a-lane widths; the other widths of
 // one column a lane take it at run time.
@@ -1648,7 +2161,29 @@ template <int GD, int Q>
 hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bool want_dwdb, hipStream_t s) {
     hipError_t e = hipSuccess;
     const int epi = (a.mask ? kBwdRelu : 0) | (a.lin_w ? kBwdLin : 0);
-    if (pl.sorted) {
+    if (pl.mfma_nbt > 0) {
+        // (planned only for a 16-bit gradient in its own dtype, no epilogue,
+        // uint8 bin indices)
+        if constexpr (GD != PLE_DTYPE_F32 && GD == Q) {
+            if (epi != 0 || idxb != 1) return hipErrorInvalidConfiguration;
+            a.db_from_buckets = 1;
+            a.fin_fused = want_dwdb && pl.C == 1;
+            const dim3 grid(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, pl.C)));
+            const TimerSlot ts = timer_slot(PLE_TIMER_BACKWARD);
+            t_slot = ts;
+            switch (pl.mfma_nbt) {
+                case 1: launch_mfma<GD, 1>(pl.mfma_nq, grid, pl.lds, s, a); break;
+                case 2: launch_mfma<GD, 2>(pl.mfma_nq, grid, pl.lds, s, a); break;
+                default: launch_mfma<GD, 3>(pl.mfma_nq, grid, pl.lds, s, a); break;
+            }
+            t_slot = TimerSlot{};
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            timer_commit(ts);
+        } else {
+            return hipErrorInvalidConfiguration;
+        }
+    } else if (pl.sorted) {
         // (linear0's bias gradient without a ReLU: the buckets sum the unmasked g)
         a.db_from_buckets = (Q == PLE_DTYPE_F32 || GD == Q) && (a.lin_w == nullptr || a.mask == nullptr);
         const dim3 grid(static_cast<unsigned>(kNumXcd * tiles_per_xcd(a.G, pl.C)));
@@ -1695,7 +2230,7 @@ hipError_t launch_typed(BwdArgs a, const BwdPlan &pl, int idxb, bool want_dx, bo
         t_slot = TimerSlot{};
         timer_commit(ts);
     }
-    if (want_dwdb && !(pl.sorted && a.fin_fused)) {
+    if (want_dwdb && !((pl.sorted || pl.mfma_nbt > 0) && a.fin_fused)) {
         size_t lds = static_cast<size_t>(a.B) * 2 * kFinStride * sizeof(float);
         a.fin_direct = lds > kLdsMax;          // very many bins: no LDS table
         if (a.fin_direct) lds = 0;
@@ -1775,14 +2310,15 @@ int backward_plan_info(const BackwardRequest &r, ple_backward_plan_info_t *info)
     const BwdPlan &pl = plan_cached(r.N, r.F, r.B, r.D, gaddr % 16 == 0, r.grad_dtype != PLE_DTYPE_F32, raw_db, lin);
     info->sorted = pl.sorted ? 1 : 0;
     info->chunks = pl.C;
-    info->features_per_group = pl.sorted ? pl.geo.FS : 1;
+    info->features_per_group = pl.sorted || pl.mfma_nbt > 0 ? pl.geo.FS : 1;
     info->columns_per_lane = pl.sorted ? pl.vec : 1;
     info->lanes_per_row = pl.sorted ? pl.geo.LGW : 1;
-    info->threads = pl.sorted ? pl.rb : kWave;
+    info->threads = pl.sorted || pl.mfma_nbt > 0 ? pl.rb : kWave;
     info->lds_bytes = pl.lds;
     info->workspace_bytes = pl.total();
     info->bins_per_window = pl.sorted ? pl.geo.BW : static_cast<int>(r.B);
     info->windows = pl.sorted ? pl.geo.NW : 1;
+    info->matrix_cores = pl.mfma_nbt > 0 ? 1 : 0;
     return PLE_OK;
 }
 
@@ -1811,7 +2347,7 @@ int backward_run(const BackwardRequest &r) {
     if (need > 0 && (r.workspace == nullptr || r.workspace_bytes < need ||
                      reinterpret_cast<uintptr_t>(r.workspace) % 256 != 0))
         return PLE_E_WORKSPACE;
-    const int64_t grid_max = pl.sorted ? kNumXcd * tiles_per_xcd(pl.geo.G, pl.C)
+    const int64_t grid_max = pl.sorted || pl.mfma_nbt > 0 ? kNumXcd * tiles_per_xcd(pl.geo.G, pl.C)
                                        : static_cast<int64_t>(r.F) * pl.C * ((r.D + kWave - 1) / kWave);
     if (grid_max > INT32_MAX) return PLE_E_TOO_LARGE;
     BwdArgs a = pl.geo;

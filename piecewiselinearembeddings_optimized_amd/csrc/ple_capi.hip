@@ -114,7 +114,7 @@ int check_common(int64_t N, int64_t F, int64_t B, int64_t D) {
 
 extern "C" {
 
-int ple_abi_version(void) { return (1 << 16) | 3; }
+int ple_abi_version(void) { return (1 << 16) | 4; }
 
 int ple_bin_index_bytes(int64_t max_n_bins) { return ple::idx_bytes_for(max_n_bins); }
 

@@ -121,7 +121,17 @@ def test_backward_plan_query_and_workspace_sizes():
     assert c1["workspace_bytes"] >= c1["chunks"] * 128 * 48 * 2 * 32 * 4
     assert capi.workspace_bytes(65536, 128, 48, 32) >= c1["workspace_bytes"]
     c4 = capi.backward_plan(8192, 1024, 96, 24, grad_dtype=torch.bfloat16)
-    assert c4["sorted"] == 1 and c4["chunks"] == 1 and c4["columns_per_lane"] == 8
+    # a 16-bit gradient in its own dtype: the matrix-core kernel, groups of
+    # four features, 512-thread workgroups, one chunk
+    assert c4["matrix_cores"] == 1 and c4["sorted"] == 0 and c4["chunks"] == 1 and c4["workspace_bytes"] == 0
+    assert c4["features_per_group"] == 4 and c4["threads"] == 512 and c4["lds_bytes"] <= 160 * 1024
+    # ... not past 96 bins, nor where it would take more than 8 chunks
+    assert capi.backward_plan(8192, 1024, 128, 24, grad_dtype=torch.bfloat16)["matrix_cores"] == 0
+    assert capi.backward_plan(65536, 32, 96, 24, grad_dtype=torch.bfloat16)["matrix_cores"] == 0
+    assert capi.backward_plan(65536, 128, 48, 32, grad_dtype=torch.bfloat16)["chunks"] == 8
+    c4s = capi.backward_plan(8192, 1024, 96, 24, grad_dtype=torch.float32, quant_dtype=torch.bfloat16)
+    assert c4s["matrix_cores"] == 0 and c4s["sorted"] == 1 and c4s["columns_per_lane"] == 4
+    assert c1["matrix_cores"] == 0
     assert c1["windows"] == 1 and c1["bins_per_window"] == 48
     with pytest.raises(capi.PleError):
         capi.backward_plan(1024, 8, 48, 24, grad_dtype=torch.bfloat16, quant_dtype=torch.float16)
