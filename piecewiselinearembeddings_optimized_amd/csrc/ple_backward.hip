@@ -1053,6 +1053,18 @@ __device__ __forceinline__ f32x16_t mfma16(uint4 a, uint4 b, f32x16_t c) {
 // the VALU write of that operand and keeps the wait states a matrix
 // instruction needs after it (an asm producer is invisible to that check)
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// c + a.lo * b.lo + a.hi * b.hi, 16-bit pairs (bf16 or fp16), fp32 sum
+template <int GD>
+__device__ __forceinline__ float dot2_16(uint32_t a, uint32_t b, float c) {
+    if constexpr (GD == PLE_DTYPE_BF16) {
+        typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a), __builtin_bit_cast(bf2, b), c, false);
+    } else {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+    }
+}
 __device__ __forceinline__ uint32_t pk_min_u16(uint32_t a, uint32_t b) {
     uint32_t r;
     __asm__("v_pk_min_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
@@ -1099,21 +1111,22 @@ constexpr int kMfmaWaveBytes = kBPW * (2 * 64 + 2 * 64) + 4 * kMB * kDxB;
 // deterministic, and no sort.
 //
 // One workgroup per (group of FS adjacent features, chunk of samples), in
-// steps of 256 / FS samples.  The workgroup loads a step together -- the FS
+// steps of 512 / FS samples.  The workgroup loads a step together -- the FS
 // rows of a sample are contiguous, so the loads cover whole runs of memory
 // (rows of 48 bytes read one feature at a time, each at its sample's stride,
-// draw about half the rate) -- into LDS, two stages deep: the rows as
-// loaded, and each 32-sample block transposed for the products; x and the
-// bin indices likewise.  Wave w takes feature w % FS and block w / FS of each
-// step, and keeps that feature's histograms (NBT tiles of 32 bins, bucket
-// and weighted) in its accumulators.  Lane l holds sample l % 32 of the
-// block, the half l / 32 of its row (4 NQ columns): its bin, q(frac) and dx
-// come out of registers -- dx as the half-row's dot product with the
-// pre-scaled weight row of its bin (plus the lower bin's for x on a left
-// edge), the two halves added low half first.  At the end the waves of a
-// feature add their histograms in LDS in wave order, and they go, like the
-// sorted path's, to dW / db (one chunk) or to the chunk partials.  Rows of
-// D = 8 NQ columns (NQ = 1..4), at most 32 NBT bins; bin indices are uint8.
+// draw about half the rate) -- into LDS, two stages deep: the rows feature
+// by feature, x, and the words holding the bin indices.  Wave w takes
+// feature w % FS and blocks 2 (w / FS) and 2 (w / FS) + 1 of each step (two
+// blocks side by side hide each other's LDS round trips), and keeps that
+// feature's histograms (NBT tiles of 32 bins, bucket and weighted) in its
+// accumulators.  Lane l holds sample l % 32 of a block, the half l / 32 of
+// its row (4 NQ columns): its bin, q(frac) and dx come out of registers --
+// dx as iw_k times the half row's dot product with q(W[k]) (plus iw_{k-1}
+// times the one with q(W[k-1]) for x on a left edge), the two halves added
+// low half first.  At the end the waves of a feature add their histograms in
+// LDS in wave order, and they go, like the sorted path's, to dW / db (one
+// chunk) or to the chunk partials.  Rows of D = 8 NQ columns (NQ = 1..4), at
+// most 32 NBT bins; bin indices are uint8.
 template <int GD, int NBT, int NQ>
 __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) {
     constexpr int D = 8 * NQ;
@@ -1139,10 +1152,10 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
     const int f = f0 + fl;
     const bool fok = f < F;
     const int n = fok ? clamp_nbins(a.nbins[f], B) : 1;
-    // the group's tables: [FS][B+1][D] q(W) * iw (row r: bin r - 1), [FS][B]
-    // iw, [FS][B+1] edges; then the two stages and the waves' areas, which
-    // the histograms [FS][B][2D] take over after the stream
-    float *s_qw = reinterpret_cast<float *>(lds + a.ro_qw) + fl * (B + 1) * D;
+    // the group's tables: [FS][B+1][D] q(W) in the 16-bit dtype (exact; row
+    // r: bin r - 1), [FS][B] iw, [FS][B+1] edges; then the two stages and the
+    // waves' areas, which the histograms [FS][B][2D] take over after the stream
+    const uint16_t *s_qh = reinterpret_cast<const uint16_t *>(lds + a.ro_qw) + fl * (B + 1) * D;
     float *s_iw = reinterpret_cast<float *>(lds + a.ro_iw) + fl * B;
     float *s_edge = reinterpret_cast<float *>(lds + a.ro_edge) + fl * (B + 1);
     float *s_hist = reinterpret_cast<float *>(lds + a.ro_hist);
@@ -1175,13 +1188,16 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
         const int j = rem - rr * D;
         const int kg = rr - 1;
         const int fa = f0 + ff;
-        float w = 0.0f;
+        uint16_t w = 0;
         if (fa < F) {
             const int na = clamp_nbins(a.nbins[fa], B);
             const int64_t fb = static_cast<int64_t>(fa) * B;
-            if (kg >= 0 && kg < na) w = quant<GD>(a.weight[(fb + phys_bin(kg, na, B)) * D + j]) * a.iw[fb + kg];
+            if (kg >= 0 && kg < na) {
+                const float v = a.weight[(fb + phys_bin(kg, na, B)) * D + j];
+                w = GD == PLE_DTYPE_BF16 ? static_cast<uint16_t>(__float_as_uint(quant<GD>(v)) >> 16) : f16_bits(v);
+            }
         }
-        reinterpret_cast<float *>(lds + a.ro_qw)[i] = w;
+        reinterpret_cast<uint16_t *>(lds + a.ro_qw)[i] = w;
     }
     for (int i = tid; i < static_cast<int>(2 * kStageBytes / 4); i += kMfmaBlock)
         reinterpret_cast<uint32_t *>(s_stage)[i] = 0u;
@@ -1284,7 +1300,7 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
         // k >= 1); the blocks' steps side by side
         int k[kBPW];
         bool valid[kBPW], edge[kBPW];
-        float qf[kBPW], dot[kBPW];
+        float qf[kBPW], dot[kBPW], iwk[kBPW];
         uint2 gv[kBPW][NQ];
         const unsigned char *rows[kBPW];
 #pragma unroll
@@ -1297,38 +1313,41 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
             k[i] = clamp_bin(static_cast<int>((kw >> kshift) & 0xffu), n);
             const float xv = st_x(buf)[(sb0 + sl) * FS + fl];
             const float e = s_edge[k[i]];
-            qf[i] = quant<GD>((xv - e) * s_iw[k[i]]);
+            iwk[i] = s_iw[k[i]];
+            qf[i] = quant<GD>((xv - e) * iwk[i]);
             edge[i] = k[i] > 0 && xv == e;
             // the lane's half row
             rows[i] = st_rows(buf, fl) + sb0 * kRowBytes;
             const unsigned char *row = rows[i] + sl * kRowBytes + h * DH * 2;
 #pragma unroll
             for (int j = 0; j < NQ; ++j) gv[i][j] = *reinterpret_cast<const uint2 *>(row + 8 * j);
-            // dx: the half row against bin k's pre-scaled weights
-            float w[DH];
-            lds_load_vec<DH>(s_qw + (k[i] + 1) * D + DH * h, w);
-            dot[i] = 0.0f;
+            // dx: iw_k times the half row's dot product with q(W[k]) (pairs of
+            // 16-bit products, exact, summed in fp32)
+            const uint16_t *wr = s_qh + (k[i] + 1) * D + DH * h;
+            float d = 0.0f;
 #pragma unroll
             for (int j = 0; j < NQ; ++j) {
-                const uint32_t wd[2] = {gv[i][j].x, gv[i][j].y};
-#pragma unroll
-                for (int t = 0; t < 4; ++t) dot[i] = fmaf(grad_elem<GD>(wd, t), w[4 * j + t], dot[i]);
+                const uint2 wv = *reinterpret_cast<const uint2 *>(wr + 4 * j);
+                d = dot2_16<GD>(gv[i][j].x, wv.x, d);
+                d = dot2_16<GD>(gv[i][j].y, wv.y, d);
             }
+            dot[i] = d * iwk[i];
         }
-        // and bin k - 1's on a left edge, in a pass taken when the wave holds one
+        // and iw_{k-1} times the one with q(W[k-1]) on a left edge, in a pass
+        // taken when the wave holds one
         if (__ballot(edge[0] || edge[kBPW - 1])) {
 #pragma unroll
             for (int i = 0; i < kBPW; ++i) {
-                float w[DH];
-                lds_load_vec<DH>(s_qw + k[i] * D + DH * h, w);
+                const int km = k[i] > 0 ? k[i] - 1 : 0;
+                const uint16_t *wr = s_qh + k[i] * D + DH * h;
                 float d2 = 0.0f;
 #pragma unroll
                 for (int j = 0; j < NQ; ++j) {
-                    const uint32_t wd[2] = {gv[i][j].x, gv[i][j].y};
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) d2 = fmaf(grad_elem<GD>(wd, t), w[4 * j + t], d2);
+                    const uint2 wv = *reinterpret_cast<const uint2 *>(wr + 4 * j);
+                    d2 = dot2_16<GD>(gv[i][j].x, wv.x, d2);
+                    d2 = dot2_16<GD>(gv[i][j].y, wv.y, d2);
                 }
-                if (edge[i]) dot[i] += d2;
+                if (edge[i]) dot[i] += d2 * s_iw[km];
             }
         }
 #pragma unroll
@@ -1766,7 +1785,7 @@ size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_
 // areas, which the histograms take over after the stream
 size_t mfma_layout(BwdArgs &g, int B, int D, int FS) {
     LdsTaker take;
-    take(g.ro_qw, 4ull * FS * (B + 1) * D);
+    take(g.ro_qw, 2ull * FS * (B + 1) * D);
     take(g.ro_iw, 4ull * FS * B);
     take(g.ro_edge, 4ull * FS * (B + 1));
     take(g.ro_desc, std::max<size_t>(2 * kStageBytes + static_cast<size_t>(kMfmaWaves) * kMfmaWaveBytes,
