@@ -774,6 +774,11 @@ bool plan_forward(int64_t N, int64_t F, int64_t B, int64_t D, int out_bytes, boo
         if (kLdsMax / pl.lds <= 2) {
             const int64_t slots = static_cast<int64_t>(kLdsMax / pl.lds) * device_cu_count();
             c = (2 * slots) / pl.G;
+            // 16-bit outputs: one round -- a workgroup writes half the bytes
+            // per pair, so its table staging and prefix pass weigh twice as
+            // much (c4's forward in the fwd+bwd step: 131 -> 120 us; c2 / c3,
+            // fp32, keep two rounds: one costs them 3 us)
+            if (out_bytes == 2) c = slots / pl.G;
             if (c < 1) c = 1;
         }
     }
