@@ -138,8 +138,10 @@ template <int Q, int OUT, int EPI, int VEC, typename IdxT, int FB, bool NT = tru
 __global__ __launch_bounds__(FB) void ple_fwd_kernel(FwdArgs a) {
     constexpr int kWaves = FB / kWave;
     // wave tiles whose x is loaded during the table staging: with 512
-    // threads (short output rows) all of a wave's tiles in the usual plans
-    constexpr int kXEarly = FB == 512 ? 16 : 1;
+    // threads (short output rows) 16 for 16-bit outputs (all of a wave's
+    // tiles in the usual plans), 8 for fp32 ones, whose tiles' stores take
+    // twice as long (fwd+bwd step: c3 136 -> 130 us with 8, c4 116 -> 123 us)
+    constexpr int kXEarly = FB == 512 ? (OUT == PLE_DTYPE_F32 ? 8 : 16) : 1;
     constexpr bool HAS_BIAS = EPI == kEpiBias || EPI == kEpiBiasRelu;
     constexpr bool LIN = EPI == kEpiLin || EPI == kEpiLinRelu;
     extern __shared__ float smem[];
