@@ -128,3 +128,37 @@ def test_mfma_backward_forced_past_eight_chunks(tune, c_oracle):
     gx, gw = ops.backward(g_h.to("cuda:0"), x, e, iw, nb, wt, idx, True, True)
     torch.cuda.synchronize()
     _check_backward(w, g_h.float().numpy(), gx, gw, None, c_oracle, quant="bf16")
+
+
+def test_mfma_backward_misaligned_bin_indices(c_oracle):
+    """Bin indices at an odd address (a view one byte into a larger buffer,
+    through the C ABI): the kernel reads the aligned word that holds each byte
+    and shifts by the byte's place, so the results equal those from an
+    aligned copy bit for bit (F = 5: a sample's bytes straddle words)."""
+    from piecewiselinearembeddings_optimized_amd import capi
+
+    n, f, bmax, d = 1024, 5, 48, 16
+    pl = capi.backward_plan(n, f, bmax, d, grad_dtype=torch.bfloat16)
+    assert pl["matrix_cores"] == 1
+    w = wide_case(n, f, bmax, d, seed=21)
+    x, e, iw, nb, wt, _ = _inputs(w)
+    _, idx = ops.forward(x, e, iw, nb, wt, torch.bfloat16)
+    raw = torch.zeros(n * f + 8, dtype=torch.uint8, device="cuda:0")
+    raw[1:1 + n * f] = idx.reshape(-1)
+    g = torch.randn((n, f, d), device="cuda:0", generator=torch.Generator("cuda:0").manual_seed(4)).to(torch.bfloat16)
+    L = capi.lib()
+    ws = torch.empty(max(pl["workspace_bytes"], 1), dtype=torch.uint8, device="cuda:0")
+    outs = []
+    for ptr in (idx.data_ptr(), raw.data_ptr() + 1):
+        gx = torch.empty((n, f), device="cuda:0")
+        gw = torch.empty((f, bmax, d), device="cuda:0")
+        gb = torch.empty((f, d), device="cuda:0")
+        rc = L.ple_backward_launch(g.data_ptr(), x.data_ptr(), e.data_ptr(), iw.data_ptr(), nb.data_ptr(),
+                                   wt.data_ptr(), ptr, gx.data_ptr(), gw.data_ptr(), gb.data_ptr(), n, f, bmax, d,
+                                   2, 2, ws.data_ptr(), pl["workspace_bytes"], torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, L.ple_error_string(rc)
+        outs.append((gx, gw, gb))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    _check_backward(w, g.float().cpu().numpy(), outs[1][0], outs[1][1], outs[1][2], c_oracle, quant="bf16")
