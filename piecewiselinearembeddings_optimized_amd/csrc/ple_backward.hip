@@ -94,7 +94,8 @@ struct BwdArgs {
     // each pair is reduced (and its dx written) by the window of its bin.
     int BW, NW;
     int ro_qw, ro_hist, ro_db, ro_iw, ro_nb, ro_desc, ro_piece, ro_npc, ro_rec, ro_rkey, ro_rfl, ro_dx,
-        ro_lw, ro_dlw, ro_xs, ro_edge, ro_cnt, ro_seg, ro_tmp;   // fused kernel LDS (ro_dx < 0: no dx staging)
+        ro_lw, ro_dlw, ro_xs, ro_edge, ro_cnt, ro_seg, ro_tmp;   // fused kernel LDS (ro_dx < 0: no dx staging;
+                                                                  // matrix-core kernel: ro_tmp its non-finite records)
 };
 
 constexpr int kP = 1024;                        // (sample, feature) pairs per sub-tile
@@ -1101,6 +1102,10 @@ constexpr size_t kStageBytes = kStageRows + 4 * kStepSamples + 4 * kStepSamples;
 // per wave, not staged: the block's bins and q(frac) bits, 16-bit, [64]
 // each (lanes 32..63 write copies to the upper half), the dx of kDxB blocks
 constexpr int kMfmaWaveBytes = kBPW * (2 * 64 + 2 * 64) + 4 * kMB * kDxB;
+// non-finite gradient values a workgroup records (with a count and, per
+// feature of the group, a mask of the columns whose records overflowed)
+constexpr int kMfmaEvents = 512;
+constexpr size_t kMfmaEvBytes = 32 + 8 * kMfmaEvents;
 
 // A gradient already in the 16-bit quantisation dtype (bf16 or fp16) makes
 // every factor of the histograms exact in that dtype: bin k's bucket sum is
@@ -1161,6 +1166,8 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
     float *s_hist = reinterpret_cast<float *>(lds + a.ro_hist);
     unsigned char *s_stage = lds + a.ro_desc;
     unsigned char *wb = lds + a.ro_desc + 2 * kStageBytes + wave * kMfmaWaveBytes;
+    uint32_t *s_evn = reinterpret_cast<uint32_t *>(lds + a.ro_tmp);   // [0] records, [4 + fl] overflow columns
+    uint2 *s_ev = reinterpret_cast<uint2 *>(lds + a.ro_tmp + 32);     // {bin | col << 8 | fl << 16, g | q << 16}
     uint16_t *s_bin = reinterpret_cast<uint16_t *>(wb);                 // [kBPW][64] bin, 0xffff past the batch
     uint16_t *s_q = reinterpret_cast<uint16_t *>(wb + kBPW * 128);      // [kBPW][64] q(frac) bits
     float *s_dxb = reinterpret_cast<float *>(wb + kBPW * 256);          // [kDxB][32] dx
@@ -1201,6 +1208,7 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
     }
     for (int i = tid; i < static_cast<int>(2 * kStageBytes / 4); i += kMfmaBlock)
         reinterpret_cast<uint32_t *>(s_stage)[i] = 0u;
+    if (tid < 8) s_evn[tid] = 0u;
     __syncthreads();
 
     // ---- the loads of a step: kBPW NQ 8-byte pieces a lane in address order -
@@ -1350,6 +1358,33 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
                 if (edge[i]) dot[i] += d2 * s_iw[km];
             }
         }
+        // Non-finite gradient values: in the products, 0 * inf would spread
+        // them to every bin of their column; they leave the block (zeros in
+        // its staged rows) and are added to their own bin's cells at the end,
+        // as the sorted path sums them.  A half row holding one has a
+        // non-finite dot product (inf times a weight is +-inf or NaN).
+        if (__ballot((valid[0] && !__builtin_isfinite(dot[0])) ||
+                     (valid[kBPW - 1] && !__builtin_isfinite(dot[kBPW - 1])))) {
+#pragma unroll
+            for (int i = 0; i < kBPW; ++i) {
+                if (!valid[i] || __builtin_isfinite(dot[i])) continue;
+                uint16_t *hr = reinterpret_cast<uint16_t *>(const_cast<unsigned char *>(rows[i]) + sl * kRowBytes +
+                                                            h * DH * 2);
+                const uint32_t qbits = GD == PLE_DTYPE_BF16 ? (__float_as_uint(qf[i]) >> 16) : f16_bits(qf[i]);
+                for (int e = 0; e < DH; ++e) {
+                    const uint32_t gb = hr[e];
+                    const uint32_t em = GD == PLE_DTYPE_BF16 ? 0x7F80u : 0x7C00u;   // exponent bits
+                    if ((gb & em) != em) continue;
+                    const int col = DH * h + e;
+                    const uint32_t slot = atomicAdd(&s_evn[0], 1u);
+                    if (slot < static_cast<uint32_t>(kMfmaEvents))
+                        s_ev[slot] = make_uint2(static_cast<uint32_t>(k[i]) | (col << 8) | (fl << 16), gb | (qbits << 16));
+                    else
+                        atomicOr(&s_evn[4 + fl], 1u << col);
+                    hr[e] = 0;
+                }
+            }
+        }
 #pragma unroll
         for (int i = 0; i < kBPW; ++i) {
             const float other = __shfl_xor(dot[i], 32);
@@ -1447,6 +1482,30 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
         }
         __syncthreads();
     }
+
+    // the recorded non-finite values into their bins' cells, in record order
+    // (inf and NaN sums do not depend on it); columns whose records
+    // overflowed become NaN
+    if (tid == 0 && (s_evn[0] | s_evn[4] | s_evn[5] | s_evn[6] | s_evn[7]) != 0u) {
+        const int ne = min(static_cast<int>(s_evn[0]), kMfmaEvents);
+        for (int e = 0; e < ne; ++e) {
+            const uint2 r = s_ev[e];
+            const int bin = r.x & 0xff, col = (r.x >> 8) & 0xff, ff = r.x >> 16;
+            const float g = GD == PLE_DTYPE_BF16 ? __uint_as_float((r.y & 0xffffu) << 16)
+                                                 : f16_to_float(static_cast<uint16_t>(r.y));
+            const float q = GD == PLE_DTYPE_BF16 ? __uint_as_float(r.y & 0xffff0000u)
+                                                 : f16_to_float(static_cast<uint16_t>(r.y >> 16));
+            float *hp = s_hist + (ff * B + bin) * D2;
+            hp[col] += g;
+            hp[D + col] += q * g;
+        }
+        for (int ff = 0; ff < FS; ++ff)
+            for (int col = 0; col < D; ++col)
+                if (s_evn[4 + ff] >> col & 1u)
+                    for (int bin = 0; bin < B; ++bin)
+                        s_hist[(ff * B + bin) * D2 + col] = s_hist[(ff * B + bin) * D2 + D + col] = __builtin_nanf("");
+    }
+    __syncthreads();
 
     if (a.fin_fused) {
         // one chunk: dW and db from the histograms (the finalize kernel's
@@ -1791,6 +1850,7 @@ size_t mfma_layout(BwdArgs &g, int B, int D, int FS) {
     take(g.ro_desc, std::max<size_t>(2 * kStageBytes + static_cast<size_t>(kMfmaWaves) * kMfmaWaveBytes,
                                      8ull * FS * B * D));
     g.ro_hist = g.ro_desc;
+    take(g.ro_tmp, kMfmaEvBytes);
     return take.off;
 }
 

@@ -162,3 +162,43 @@ def test_mfma_backward_misaligned_bin_indices(c_oracle):
     for a, b in zip(*outs):
         assert torch.equal(a, b)
     _check_backward(w, g.float().cpu().numpy(), outs[1][0], outs[1][1], outs[1][2], c_oracle, quant="bf16")
+
+
+def _same_class(a, b):
+    """Same NaN / +inf / -inf positions, and the finite values at the fp32 bar
+    of their magnitude."""
+    a, b = a.float().cpu(), b.float().cpu()
+    assert torch.equal(torch.isnan(a), torch.isnan(b))
+    assert torch.equal(torch.isposinf(a), torch.isposinf(b)) and torch.equal(torch.isneginf(a), torch.isneginf(b))
+    fin = torch.isfinite(a)
+    scale = b[fin].abs().max().clamp_min(1e-30) if fin.any() else torch.tensor(1.0)
+    assert torch.allclose(a[fin], b[fin], rtol=1e-5, atol=1e-5 * float(scale))
+
+
+@pytest.mark.parametrize("quant", ["bf16", "f16"])
+def test_mfma_backward_non_finite_gradients(quant, tune):
+    """inf, -inf and NaN in the gradient stay in their own bin's cells (as
+    the sorted path sums them): dx, dW and db have the sorted path's NaN /
+    inf pattern, and its finite values."""
+    from piecewiselinearembeddings_optimized_amd import capi
+
+    n, f, bmax, d = 2048, 8, 96, 24
+    qt = QT[quant]
+    assert capi.backward_plan(n, f, bmax, d, grad_dtype=qt)["matrix_cores"] == 1
+    w = wide_case(n, f, bmax, d, seed=31)
+    x, e, iw, nb, wt, _ = _inputs(w)
+    _, idx = ops.forward(x, e, iw, nb, wt, qt)
+    g = torch.randn((n, f, d), device="cuda:0", generator=torch.Generator("cuda:0").manual_seed(9)).to(qt)
+    for (s, ff, c), v in (((5, 3, 7), float("inf")), ((100, 3, 2), float("-inf")), ((700, 6, 20), float("nan")),
+                          ((701, 6, 20), float("inf")), ((1500, 0, 0), float("inf")), ((1501, 0, 0), float("-inf")),
+                          ((2047, 7, 23), float("nan"))):
+        g[s, ff, c] = v
+    gx, gw = ops.backward(g, x, e, iw, nb, wt, idx, True, True)
+    _, _, gb = ops.backward_with_bias(g, x, e, iw, nb, wt, idx, qt, False, False, True)
+    tune("BWD_MFMA", 1)
+    sx, sw = ops.backward(g, x, e, iw, nb, wt, idx, True, True)
+    _, _, sb = ops.backward_with_bias(g, x, e, iw, nb, wt, idx, qt, False, False, True)
+    torch.cuda.synchronize()
+    for got, ref in ((gx, sx), (gw, sw), (gb, sb)):
+        _same_class(got, ref)
+    assert not torch.isfinite(gw).all() and torch.isfinite(gw[1]).all()   # feature 1 holds no non-finite value
