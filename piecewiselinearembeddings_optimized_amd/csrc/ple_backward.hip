@@ -1027,6 +1027,18 @@ __global__ __launch_bounds__(RB, 2) void ple_bwd_fused_kernel(BwdArgs a) {
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef short v8s_t __attribute__((ext_vector_type(8)));
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+
+// gfx950's transposing LDS read: within each group of 16 lanes, lane r
+// addresses 4 consecutive 16-bit elements (a row of a 16 x 4 block, 8-byte
+// aligned) and lane j receives element j % 4 of rows j / 4, j / 4 + 4,
+// j / 4 + 8, j / 4 + 12 (the mapping checked on an MI355X).  With lane r
+// addressing sample s0 + r / 4, columns 4 (r % 4) .. of a row-major block,
+// lane j receives column j of samples s0 .. s0 + 3.
+__device__ __forceinline__ v4s_t lds_read_tr16(const short *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4s_t *)(const_cast<short *>(p)));
+}
 
 // C += A B on a 32x32x16 matrix instruction, 16-bit operands, fp32
 // accumulation: A 32 x 16, lane l holding A[l % 32][8 (l / 32) + t] in its
@@ -1273,6 +1285,10 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
     // ---- the wave's block of each step --------------------------------------
     const int sl = lane % 32;   // the lane's sample in a block
     const int h = lane / 32;    // and its half row: columns DH h .. DH h + DH - 1
+    // the transposing reads of the products' B operand: lane l of group
+    // l / 16 addresses sample 8 h + (l % 16) / 4 (+ 4 for the second read),
+    // columns 16 ((l / 16) % 2) + 4 (l % 4) .. of the block's staged rows
+    const int tr_off = (8 * h + (lane % 16) / 4) * kRowCols + 16 * ((lane / 16) % 2) + 4 * (lane % 4);
     f32x16_t hb[NBT], hw[NBT];
 #pragma unroll
     for (int T = 0; T < NBT; ++T)
@@ -1396,16 +1412,17 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
         }
         // the histograms: two steps of 16 samples a block; A = the one-hot
         // (and q-weighted one-hot) rows of this lane's bins, B = the gradient:
-        // column sl of samples sb .. sb + 7 (zero past D)
+        // column sl of samples sb .. sb + 7 (zero past D), by two transposing
+        // LDS reads of 4 samples each
 #pragma unroll
         for (int i = 0; i < kBPW; ++i) {
-            const uint16_t *gcol = reinterpret_cast<const uint16_t *>(rows[i]) + sl;
+            const short *gtr = reinterpret_cast<const short *>(rows[i]) + tr_off;
 #pragma unroll
             for (int ks = 0; ks < kMB / 16; ++ks) {
                 const int sb = 16 * ks + 8 * h;
-                v8s_t bv;
-#pragma unroll
-                for (int t = 0; t < 8; ++t) bv[t] = static_cast<short>(gcol[(sb + t) * kRowCols]);
+                const v4s_t lo = lds_read_tr16(gtr + 16 * ks * kRowCols);
+                const v4s_t hi = lds_read_tr16(gtr + (16 * ks + 4) * kRowCols);
+                const v8s_t bv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 const uint4 bop = __builtin_bit_cast(uint4, bv);
                 const uint4 kb = *reinterpret_cast<const uint4 *>(s_bin + i * 64 + sb);
                 const uint4 qb = *reinterpret_cast<const uint4 *>(s_q + i * 64 + sb);
