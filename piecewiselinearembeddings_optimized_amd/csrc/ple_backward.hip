@@ -134,29 +134,31 @@ constexpr int kFinLanes = kBlock / kFinCols;   // lanes per column (half a wave)
 // between slots) or null.  Returns the lanes' running sums: lane 0 holds the
 // column's bucket total.  Every lane of the group takes part (a lane with
 // n = 0 adds zeros), so the shuffles see live lanes.  A fixed order: results
-// repeat bitwise.
-template <typename Total>
+// repeat bitwise.  LANES: lanes a column (a power of two up to a wave).
+template <int LANES = kFinLanes, typename Total>
 __device__ __forceinline__ float dw_suffix(Total total, int n, int B, int D, int l, float *dw) {
-    const int m = (n + kFinLanes - 1) / kFinLanes;   // bins per lane
+    const int m = (n + LANES - 1) / LANES;   // bins per lane
     const int lo = min(n, l * m);
     const int hi = min(n, lo + m);
     float run = 0.0f;
+#pragma unroll 4
     for (int k = hi - 1; k >= lo; --k) run += total(k, 0);
     // inclusive suffix over the lanes: sum of the runs of lanes l, l+1, ...
     float incl = run;
 #pragma unroll
-    for (int off = 1; off < kFinLanes; off <<= 1) {
-        const float t = __shfl_down(incl, off, kFinLanes);
-        if (l + off < kFinLanes) incl += t;
+    for (int off = 1; off < LANES; off <<= 1) {
+        const float t = __shfl_down(incl, off, LANES);
+        if (l + off < LANES) incl += t;
     }
-    const float above = __shfl_down(incl, 1, kFinLanes);
+    const float above = __shfl_down(incl, 1, LANES);
     if (dw) {
-        float fut = l + 1 < kFinLanes ? above : 0.0f;
+        float fut = l + 1 < LANES ? above : 0.0f;
+#pragma unroll 4
         for (int k = hi - 1; k >= lo; --k) {
             dw[static_cast<int64_t>(phys_bin(k, n, B)) * D] = total(k, 1) + fut;
             fut += total(k, 0);
         }
-        for (int k = n - 1 + l; k < B - 1; k += kFinLanes) dw[static_cast<int64_t>(k) * D] = 0.0f;
+        for (int k = n - 1 + l; k < B - 1; k += LANES) dw[static_cast<int64_t>(k) * D] = 0.0f;
     }
     return incl;
 }
@@ -1118,6 +1120,13 @@ constexpr int kMfmaWaveBytes = kBPW * (2 * 64 + 2 * 64) + 4 * kMB * kDxB;
 // feature of the group, a mask of the columns whose records overflowed)
 constexpr int kMfmaEvents = 512;
 constexpr size_t kMfmaEvBytes = 32 + 8 * kMfmaEvents;
+constexpr int kMfmaMaxBins = 96;   // three tiles of 32 bins
+constexpr int kTabLoads = 16;      // table loads a thread has in flight in the set-up
+constexpr int kMfmaFinLanes = 4;   // lanes of a (feature, column) in the kernel's dW / db step
+// the set-up reads a group's iw and edges one entry a thread, and clears the
+// stages 16 bytes at a time
+static_assert(4 * (kMfmaMaxBins + 1) <= kMfmaBlock, "iw / edge tables: one entry a thread");
+static_assert(kStageBytes % 16 == 0, "stages cleared in 16-byte stores");
 
 // A gradient already in the 16-bit quantisation dtype (bf16 or fp16) makes
 // every factor of the histograms exact in that dtype: bin k's bucket sum is
@@ -1168,7 +1177,7 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
     const int f0 = fg * FS;
     const int f = f0 + fl;
     const bool fok = f < F;
-    const int n = fok ? clamp_nbins(a.nbins[f], B) : 1;
+    const int n = fok ? clamp_nbins(a.nbins[f], B) : 1;   // the wave's feature's bins
     // the group's tables: [FS][B+1][D] q(W) in the 16-bit dtype (exact; row
     // r: bin r - 1), [FS][B] iw, [FS][B+1] edges; then the two stages and the
     // waves' areas, which the histograms [FS][B][2D] take over after the stream
@@ -1189,39 +1198,6 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
     auto st_k = [&](int buf) {
         return reinterpret_cast<uint32_t *>(s_stage + buf * kStageBytes + kStageRows + 4 * kStepSamples);
     };
-
-    // ---- tables; the transposed blocks' columns past D stay zero ----------
-    for (int i = tid; i < FS * B; i += kMfmaBlock) {
-        const int ff = f0 + i / B;
-        reinterpret_cast<float *>(lds + a.ro_iw)[i] = ff < F ? a.iw[static_cast<int64_t>(ff) * B + i % B] : 0.0f;
-    }
-    for (int i = tid; i < FS * (B + 1); i += kMfmaBlock) {
-        const int ff = f0 + i / (B + 1);
-        reinterpret_cast<float *>(lds + a.ro_edge)[i] =
-            ff < F ? a.edges[static_cast<int64_t>(ff) * (B + 1) + i % (B + 1)] : 0.0f;
-    }
-    for (int i = tid; i < FS * (B + 1) * D; i += kMfmaBlock) {
-        const int ff = i / ((B + 1) * D);
-        const int rem = i - ff * (B + 1) * D;
-        const int rr = rem / D;
-        const int j = rem - rr * D;
-        const int kg = rr - 1;
-        const int fa = f0 + ff;
-        uint16_t w = 0;
-        if (fa < F) {
-            const int na = clamp_nbins(a.nbins[fa], B);
-            const int64_t fb = static_cast<int64_t>(fa) * B;
-            if (kg >= 0 && kg < na) {
-                const float v = a.weight[(fb + phys_bin(kg, na, B)) * D + j];
-                w = GD == PLE_DTYPE_BF16 ? static_cast<uint16_t>(__float_as_uint(quant<GD>(v)) >> 16) : f16_bits(v);
-            }
-        }
-        reinterpret_cast<uint16_t *>(lds + a.ro_qw)[i] = w;
-    }
-    for (int i = tid; i < static_cast<int>(2 * kStageBytes / 4); i += kMfmaBlock)
-        reinterpret_cast<uint32_t *>(s_stage)[i] = 0u;
-    if (tid < 8) s_evn[tid] = 0u;
-    __syncthreads();
 
     // ---- the loads of a step: kBPW NQ 8-byte pieces a lane in address order -
     // piece u = tid + kMfmaBlock r of the step's SPS x FS D / 4 pieces:
@@ -1269,6 +1245,61 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
         const uint8_t *kb8 = static_cast<const uint8_t *>(a.idx) + pair;
         pk[p] = *reinterpret_cast<const uint32_t *>(kb8 - (reinterpret_cast<uintptr_t>(kb8) & 3));
     };
+    // the first step's loads go out before the tables' (the stream's first
+    // wait overlaps the set-up)
+#pragma unroll
+    for (int p = 0; p < kMfmaPF; ++p) load_step(p, p);
+
+    // ---- tables; the transposed blocks' columns past D stay zero ----------
+    // Every load of the set-up is unconditional (an entry that does not exist
+    // reads entry 0 and is replaced by zero) and issued in rounds of kTabLoads
+    // before the round's first use: the set-up waits for the memory a few
+    // times, not once or twice per entry.
+    int nfe[4];   // the group's features' bin counts (0 past F)
+#pragma unroll
+    for (int ff = 0; ff < 4; ++ff) nfe[ff] = ff < FS && f0 + ff < F ? clamp_nbins(a.nbins[f0 + ff], B) : 0;
+    auto nbins_of = [&](int ff) __attribute__((always_inline)) {
+        return ff == 0 ? nfe[0] : ff == 1 ? nfe[1] : ff == 2 ? nfe[2] : nfe[3];
+    };
+    {
+        // iw and edges: FS (B + 1) <= 4 * 97 entries, one a thread
+        const bool iok = tid < FS * B && f0 + tid / B < F;
+        const bool eok = tid < FS * (B + 1) && f0 + tid / (B + 1) < F;
+        const float iv = a.iw[iok ? static_cast<int64_t>(f0) * B + tid : 0];
+        const float ev = a.edges[eok ? static_cast<int64_t>(f0) * (B + 1) + tid : 0];
+        const int ntab = FS * (B + 1) * D;
+        for (int i0 = 0; i0 < ntab; i0 += kTabLoads * kMfmaBlock) {
+            float wv[kTabLoads];
+            bool wok[kTabLoads];
+#pragma unroll
+            for (int u = 0; u < kTabLoads; ++u) {
+                const int i = i0 + u * kMfmaBlock + tid;
+                const int ff = i / ((B + 1) * D);
+                const int rem = i - ff * (B + 1) * D;
+                const int rr = rem / D;
+                const int j = rem - rr * D;
+                const int kg = rr - 1;
+                const int na = nbins_of(ff);
+                wok[u] = i < ntab && kg >= 0 && kg < na;
+                wv[u] = a.weight[wok[u] ? ((static_cast<int64_t>(f0 + ff) * B + phys_bin(kg, na, B)) * D + j) : 0];
+            }
+#pragma unroll
+            for (int u = 0; u < kTabLoads; ++u) {
+                const int i = i0 + u * kMfmaBlock + tid;
+                const uint16_t w = !wok[u] ? 0
+                                   : GD == PLE_DTYPE_BF16 ? static_cast<uint16_t>(__float_as_uint(quant<GD>(wv[u])) >> 16)
+                                                          : f16_bits(wv[u]);
+                if (i < ntab) reinterpret_cast<uint16_t *>(lds + a.ro_qw)[i] = w;
+            }
+        }
+        if (tid < FS * B) reinterpret_cast<float *>(lds + a.ro_iw)[tid] = iok ? iv : 0.0f;
+        if (tid < FS * (B + 1)) reinterpret_cast<float *>(lds + a.ro_edge)[tid] = eok ? ev : 0.0f;
+    }
+    for (int i = tid; i < static_cast<int>(2 * kStageBytes / 16); i += kMfmaBlock)
+        reinterpret_cast<uint4 *>(s_stage)[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid < 8) s_evn[tid] = 0u;
+    __syncthreads();
+
     // a step's loads into LDS stage buf: the rows, feature by feature, x,
     // the index words (or bytes)
     auto stage_step = [&](int p, int buf) __attribute__((always_inline)) {
@@ -1456,8 +1487,6 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
     // (stage buf is rewritten two steps later, after the next step's barrier:
     // every wave has left this step's blocks by then)
     const bool mine = fok;
-#pragma unroll
-    for (int p = 0; p < kMfmaPF; ++p) load_step(p, p);
     int st = 0;
     for (; st + 1 < nsteps; st += 2) {
 #pragma unroll
@@ -1526,27 +1555,28 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
 
     if (a.fin_fused) {
         // one chunk: dW and db from the histograms (the finalize kernel's
-        // steps), one (feature, column) per group of kFinLanes lanes
-        constexpr int kGroups = kMfmaBlock / kFinLanes;
-        const int l = tid % kFinLanes;
+        // steps), one (feature, column) per kMfmaFinLanes lanes: the FS D <=
+        // 128 columns of the group in one round
+        constexpr int kGroups = kMfmaBlock / kMfmaFinLanes;
+        const int l = tid % kMfmaFinLanes;
         for (int p0 = 0; p0 < FS * D; p0 += kGroups) {
-            const int pr = p0 + tid / kFinLanes;
+            const int pr = p0 + tid / kMfmaFinLanes;
             const int ff = pr / D;
             const int fa = f0 + ff;
             const bool ok = pr < FS * D && fa < F;
             const int j = ok ? pr - ff * D : 0;
-            const int nn = ok ? clamp_nbins(a.nbins[fa], B) : 0;
+            const int nn = ok ? nbins_of(ff) : 0;
             const float *hp = s_hist + (ok ? ff : 0) * B * D2 + j;
             auto total = [&](int k, int hh) __attribute__((always_inline)) { return hp[k * D2 + hh * D]; };
             float *dwc = ok && a.dw ? a.dw + static_cast<int64_t>(fa) * B * D + j : nullptr;
-            const float incl = dw_suffix(total, nn, B, D, l, dwc);
+            const float incl = dw_suffix<kMfmaFinLanes>(total, nn, B, D, l, dwc);
             if (ok && l == 0 && a.db) a.db[static_cast<int64_t>(fa) * D + j] = incl;
         }
         return;
     }
     if (a.part) {
         for (int ff = 0; ff < FS && f0 + ff < F; ++ff) {
-            const int nn = clamp_nbins(a.nbins[f0 + ff], B);
+            const int nn = nbins_of(ff);
             float *dst = a.part + (static_cast<int64_t>(c) * F + f0 + ff) * B * D2;
             for (int i = tid; i < nn * D2; i += kMfmaBlock) dst[i] = s_hist[ff * B * D2 + i];
         }
@@ -1891,7 +1921,7 @@ BwdPlan plan_backward(int64_t N, int64_t F, int64_t B, int64_t D, bool g_align16
     // cost more than the sorted path (knob PLE_TUNE_BWD_MFMA: 1 never, 2
     // whenever the shape allows).
     const int mfma_knob = tuning(PLE_TUNE_BWD_MFMA);
-    if (g16 && !raw_db && !lin && g_align16 && D % 8 == 0 && D <= 32 && B <= 96 &&
+    if (g16 && !raw_db && !lin && g_align16 && D % 8 == 0 && D <= 32 && B <= kMfmaMaxBins &&
         static_cast<int64_t>(kStepSamples) * F * D * 2 < INT32_MAX && mfma_knob != 1 &&
         tuning(PLE_TUNE_BWD_SIMPLE) == 0) {
         BwdArgs geo{};
