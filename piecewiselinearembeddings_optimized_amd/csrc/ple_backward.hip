@@ -1434,9 +1434,13 @@ __global__ __launch_bounds__(kMfmaBlock, 1) void ple_bwd_mfma_kernel(BwdArgs a) 
         }
 #pragma unroll
         for (int i = 0; i < kBPW; ++i) {
-            const float other = __shfl_xor(dot[i], 32);
-            // the same value from both halves
-            s_dxb[(nbuf * kBPW + i) * kMB + sl] = h == 0 ? dot[i] + other : other + dot[i];
+            // the two halves' sums, low half first, in every lane: gfx950's
+            // v_permlane32_swap (a VALU exchange of the wave's halves, no LDS
+            // round trip) gives lane l the value of lane l % 32 and of lane
+            // l % 32 + 32 (the mapping checked on an MI355X)
+            const uint32_t db = __float_as_uint(dot[i]);
+            const auto halves = __builtin_amdgcn_permlane32_swap(db, db, false, false);
+            s_dxb[(nbuf * kBPW + i) * kMB + sl] = __uint_as_float(halves[0]) + __uint_as_float(halves[1]);
             s_bin[i * 64 + lane] = static_cast<uint16_t>(valid[i] ? k[i] : 0xffff);
             s_q[i * 64 + lane] =
                 GD == PLE_DTYPE_BF16 ? static_cast<uint16_t>(__float_as_uint(qf[i]) >> 16) : f16_bits(qf[i]);
