@@ -1890,9 +1890,9 @@ size_t reduce_layout(BwdArgs &g, int FS, int B, int D, int LG, int PM, bool raw_
     return take.off;
 }
 
-// LDS of the matrix-core kernel: tables, the histogram, the waves' blocks
-// LDS of the matrix-core kernel: the FS features' tables, then the waves'
-// areas, which the histograms take over after the stream
+// LDS of the matrix-core kernel: the FS features' tables, then the two
+// stages and the waves' areas, which the histograms take over after the
+// stream, then the non-finite records
 size_t mfma_layout(BwdArgs &g, int B, int D, int FS) {
     LdsTaker take;
     take(g.ro_qw, 2ull * FS * (B + 1) * D);
