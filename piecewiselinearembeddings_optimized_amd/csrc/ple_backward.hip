@@ -124,6 +124,7 @@ constexpr int kFinCols = 8;
 constexpr int kFinStride = kFinCols + 1;
 constexpr int kFinLoadsInline = 128;   // chunk-sum loads per finalize thread, at most
 constexpr int kFinLanes = kBlock / kFinCols;   // lanes per column (half a wave)
+constexpr int kFinBatch = 8;                     // partial-sum elements a finalize thread loads together
 
 // One column's dW from its per-bin sums, by kFinLanes lanes (l: this lane's
 // place among them): each lane sums the buckets of its run of the n bins, a
@@ -1787,18 +1788,49 @@ __global__ __launch_bounds__(kBlock) void ple_bwd_finalize_kernel(BwdArgs a) {
     const int nsum = a.fin_summed ? 1 : a.Cd;
     const int64_t cstride = static_cast<int64_t>(a.F) * B * D2;
     if (need_tot) {
-        // element e -> (bin k, half h: bucket / weighted, column j0 + c)
-        for (int e = tid; e < n * 2 * kFinCols; e += kBlock) {
-            const int k = e / (2 * kFinCols);
-            const int h = (e / kFinCols) & 1;
-            const int cidx = e % kFinCols;
-            float sum = 0.0f;
-            if (cidx < nc) {
-                const float *p = src + k * D2 + h * D + j0 + cidx;
-#pragma unroll 8
-                for (int cc = 0; cc < nsum; ++cc) sum += p[cc * cstride];
+        // element e -> (bin k, half h: bucket / weighted, column j0 + c); a
+        // thread's kFinBatch elements load together, four chunks at a time
+        // (each element still summed in chunk order), so the loads of a
+        // batch wait for the memory once per four chunks, not once per load
+        const int ne = n * 2 * kFinCols;
+        for (int e0 = 0; e0 < ne; e0 += kFinBatch * kBlock) {
+            const float *pe[kFinBatch];
+            bool ok[kFinBatch];
+            float sum[kFinBatch];
+#pragma unroll
+            for (int u = 0; u < kFinBatch; ++u) {
+                const int e = e0 + u * kBlock + tid;
+                const int k = e / (2 * kFinCols);
+                const int h = (e / kFinCols) & 1;
+                const int cidx = e % kFinCols;
+                ok[u] = e < ne && cidx < nc;
+                pe[u] = src + (ok[u] ? k * D2 + h * D + j0 + cidx : 0);   // (else a valid address, ignored)
+                sum[u] = 0.0f;
             }
-            tot[(k * 2 + h) * kFinStride + cidx] = sum;
+            int cc = 0;
+            for (; cc + 4 <= nsum; cc += 4) {
+                float v[4][kFinBatch];
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int u = 0; u < kFinBatch; ++u) v[t][u] = pe[u][(cc + t) * cstride];
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int u = 0; u < kFinBatch; ++u) sum[u] += v[t][u];
+            }
+            for (; cc < nsum; ++cc) {
+                float v[kFinBatch];
+#pragma unroll
+                for (int u = 0; u < kFinBatch; ++u) v[u] = pe[u][cc * cstride];
+#pragma unroll
+                for (int u = 0; u < kFinBatch; ++u) sum[u] += v[u];
+            }
+#pragma unroll
+            for (int u = 0; u < kFinBatch; ++u) {
+                const int e = e0 + u * kBlock + tid;
+                if (e < ne) tot[(e / kFinCols) * kFinStride + e % kFinCols] = ok[u] ? sum[u] : 0.0f;
+            }
         }
         __syncthreads();
     }
