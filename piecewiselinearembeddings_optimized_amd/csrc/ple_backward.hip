@@ -1101,7 +1101,9 @@ constexpr int kMfmaWaves = 8;                      // waves per workgroup
 constexpr int kMfmaBlock = kMfmaWaves * kWave;
 constexpr int kMfmaPF = 1;                         // steps whose loads are in flight (1 or 2)
 constexpr int kBPW = 2;                            // blocks of a wave in a step (worked on together)
-constexpr int kDxB = 16;                           // blocks whose dx a wave stores together
+// blocks whose dx a wave stores together (c4, the whole kernel: 8 -> 211,
+// 16 -> 216, 32 -> 223, 4 -> 228 us)
+constexpr int kDxB = 8;
 // a staged row: 36 16-bit columns (72 bytes: the 8-byte reads of 32
 // consecutive rows meet distinct banks; columns D..35 stay zero, the
 // products' columns past D); a feature's rows of a step, then 32 bytes
