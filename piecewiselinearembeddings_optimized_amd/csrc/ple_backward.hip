@@ -1124,7 +1124,9 @@ constexpr int kMfmaWaveBytes = kBPW * (2 * 64 + 2 * 64) + 4 * kMB * kDxB;
 constexpr int kMfmaEvents = 512;
 constexpr size_t kMfmaEvBytes = 32 + 8 * kMfmaEvents;
 constexpr int kMfmaMaxBins = 96;   // three tiles of 32 bins
-constexpr int kTabLoads = 16;      // table loads a thread has in flight in the set-up
+// table loads a thread has in flight in the set-up (c4, the whole kernel:
+// 4 / 8 -> 203-204 us, 16 -> 209-211, 32 -> 213-215)
+constexpr int kTabLoads = 8;
 constexpr int kMfmaFinLanes = 4;   // lanes of a (feature, column) in the kernel's dW / db step
 // the set-up reads a group's iw and edges one entry a thread, and clears the
 // stages 16 bytes at a time
